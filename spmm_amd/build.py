@@ -1,0 +1,80 @@
+"""In-tree build of the native parts of spmm_amd.
+
+Two artefacts, both next to this file:
+
+* ``libspmm_amd.so`` -- the HIP kernels and the C ABI of ``include/spmm_amd.h``,
+  compiled by hipcc for gfx950 only;
+* ``_core.<abi>.so`` -- the pybind11 host layer (format builders, CPU ops, GPU
+  glue), compiled by g++ and linked against ``libspmm_amd.so`` through an
+  ``$ORIGIN`` rpath.
+
+``python -m spmm_amd.build`` rebuilds both.  Nothing is JIT-compiled at import
+time: ``spmm_amd`` loads what is here and fails loudly when it is missing.
+"""
+
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+import sysconfig
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+ROOT = HERE.parent
+CSRC = HERE / 'csrc'
+INCLUDE = ROOT / 'include'
+
+HIP_LIB = HERE / 'libspmm_amd.so'
+CORE_LIB = HERE / ('_core' + sysconfig.get_config_var('EXT_SUFFIX'))
+
+ARCH = os.environ.get('SPMM_AMD_ARCH', 'gfx950')
+
+# Packed-FP32 instructions are disabled for all device code: hipcc -O3 would
+# otherwise form v_pk_{add,mul,fma}_f32 from plain float code.
+HIPCC_FLAGS = [
+    '-O3', '-std=c++17', f'--offload-arch={ARCH}', '-fPIC', '-shared',
+    '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
+    '-Wall', '-Wno-unused-function',
+]
+
+# -ffp-contract=off keeps the CPU ops' y += a*x as a separate multiply and add,
+# the rounding of the reference's CPU loops.
+CXX_FLAGS = ['-O3', '-std=c++17', '-fPIC', '-shared', '-ffp-contract=off', '-fvisibility=hidden']
+
+
+def _run(cmd):
+    print('+', ' '.join(str(c) for c in cmd), flush=True)
+    subprocess.run([str(c) for c in cmd], check=True)
+
+
+def _hipcc():
+    for cand in (os.environ.get('HIPCC'), '/opt/rocm/bin/hipcc', 'hipcc'):
+        if cand and (os.path.sep not in cand or Path(cand).exists()):
+            return cand
+    return 'hipcc'
+
+
+def build_hip():
+    src = CSRC / 'spmm_kernels.hip'
+    _run([_hipcc(), *HIPCC_FLAGS, f'-I{INCLUDE}', src, '-o', HIP_LIB])
+
+
+def build_core():
+    import pybind11
+    src = CSRC / 'core.cpp'
+    py_inc = sysconfig.get_paths()['include']
+    _run(['g++', *CXX_FLAGS, f'-I{INCLUDE}', f'-I{CSRC}', f'-I{pybind11.get_include()}',
+          f'-I{py_inc}', src, '-o', CORE_LIB, f'-L{HERE}', '-lspmm_amd',
+          "-Wl,-rpath,$ORIGIN"])
+
+
+def build_all():
+    build_hip()
+    build_core()
+
+
+if __name__ == '__main__':
+    which = sys.argv[1:] or ['all']
+    for w in which:
+        {'all': build_all, 'hip': build_hip, 'core': build_core}[w]()

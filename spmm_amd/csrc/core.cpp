@@ -1,0 +1,401 @@
+// spmm_amd._core -- the pybind11 host layer.
+//
+// Mirrors the module surface of the reference's torch_fast_spdmm_core
+// (bindings/bindings.cpp:157-232): csr_to_boo / boo_to_csr / the CPU BOO op,
+// csr_to_pbr / pbr_to_csr / the CPU PBR op, and the GPU entry points.  It
+// holds no tensors: Python hands over numpy arrays for host work and raw
+// device pointers + a hipStream_t for GPU work, and the GPU calls go through
+// the C ABI of libspmm_amd.so (include/spmm_amd.h).
+#include <pybind11/numpy.h>
+#include <pybind11/pybind11.h>
+#include <pybind11/stl.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "formats.hpp"
+#include "spmm_amd.h"
+
+namespace py = pybind11;
+
+namespace {
+
+// Hand a vector to numpy without copying: the array owns it via a capsule.
+template <typename T>
+py::array_t<T> give(std::vector<T>&& v) {
+    auto* heap = new std::vector<T>(std::move(v));
+    py::capsule owner(heap, [](void* p) { delete static_cast<std::vector<T>*>(p); });
+    return py::array_t<T>({(py::ssize_t)heap->size()}, {(py::ssize_t)sizeof(T)}, heap->data(), owner);
+}
+
+template <typename T>
+const T* ptr_of(const py::array& a, const char* name) {
+    if (!py::isinstance<py::array_t<T>>(a) || !(a.flags() & py::array::c_style))
+        throw std::invalid_argument(std::string(name) + ": expected a contiguous array of the right dtype");
+    return static_cast<const T*>(a.data());
+}
+
+template <typename T>
+T* mut_ptr_of(py::array& a, const char* name) {
+    if (!py::isinstance<py::array_t<T>>(a) || !(a.flags() & py::array::c_style) || !a.writeable())
+        throw std::invalid_argument(std::string(name) + ": expected a writable contiguous array");
+    return static_cast<T*>(a.mutable_data());
+}
+
+bool is_i64(const py::array& a) { return a.dtype().is(py::dtype::of<int64_t>()); }
+bool is_f64(const py::array& a) { return a.dtype().is(py::dtype::of<double>()); }
+
+void raise_status(int rc) {
+    if (rc == SPMM_OK) return;
+    const std::string msg = spmm_last_error();
+    if (rc == SPMM_EINVAL || rc == SPMM_EUNSUPPORTED) throw std::invalid_argument(msg);
+    throw std::runtime_error(msg);
+}
+
+// ---------------------------------------------------------------- BOO host
+template <typename I, typename S>
+py::dict boo_build_t(const py::array& indptr, const py::array& indices, const py::array& data,
+                     int64_t rows, int64_t cols, const py::array& rl, const py::array& cl,
+                     int policy, int64_t threshold, int order) {
+    const I* ip = ptr_of<I>(indptr, "indptr");
+    const I* ix = ptr_of<I>(indices, "indices");
+    const S* dv = ptr_of<S>(data, "data");
+    const int32_t* rlp = ptr_of<int32_t>(rl, "row_labels");
+    const int32_t* clp = ptr_of<int32_t>(cl, "col_labels");
+    if ((int64_t)rl.size() != rows || (int64_t)cl.size() != cols)
+        throw std::invalid_argument("csr_to_boo: label array length must match matrix dims");
+    if ((int64_t)indptr.size() != rows + 1)
+        throw std::invalid_argument("csr_to_boo: indptr must have rows+1 entries");
+    spmm::BooArrays<I, S> A;
+    {
+        py::gil_scoped_release nogil;
+        A = spmm::build_boo<I, S>(ip, ix, dv, (I)rows, (I)cols, rlp, clp, policy, (I)threshold, order);
+    }
+    py::dict d;
+    d["rows"] = (int64_t)A.rows;
+    d["cols"] = (int64_t)A.cols;
+    d["total_nnz"] = (int64_t)A.total_nnz;
+    d["max_nr"] = (int64_t)A.max_nr;
+    d["max_nc"] = (int64_t)A.max_nc;
+    d["max_nnz_blk"] = (int64_t)A.max_nnz_blk;
+    d["nz_order"] = A.nz_order;
+    d["row_grp_ptr"] = give(std::move(A.row_grp_ptr));
+    d["row_ids"] = give(std::move(A.row_ids));
+    d["col_grp_ptr"] = give(std::move(A.col_grp_ptr));
+    d["col_ids"] = give(std::move(A.col_ids));
+    d["blk_row_grp"] = give(std::move(A.blk_row_grp));
+    d["blk_col_grp"] = give(std::move(A.blk_col_grp));
+    d["blk_nz_ptr"] = give(std::move(A.blk_nz_ptr));
+    d["blk_shift"] = give(std::move(A.blk_shift));
+    d["nz_idx"] = give(std::move(A.nz_idx));
+    d["nz_val"] = give(std::move(A.nz_val));
+    d["rem_indptr"] = give(std::move(A.rem_indptr));
+    d["rem_col_ind"] = give(std::move(A.rem_col_ind));
+    d["rem_vals"] = give(std::move(A.rem_vals));
+    d["tail_row"] = give(std::move(A.tail_row));
+    d["tail_col"] = give(std::move(A.tail_col));
+    d["tail_val"] = give(std::move(A.tail_val));
+    return d;
+}
+
+py::dict boo_build(const py::array& indptr, const py::array& indices, const py::array& data,
+                   int64_t rows, int64_t cols, const py::array& rl, const py::array& cl, int policy,
+                   int64_t threshold, int order) {
+    const bool i64 = is_i64(indptr), f64 = is_f64(data);
+    if (i64 && f64) return boo_build_t<int64_t, double>(indptr, indices, data, rows, cols, rl, cl, policy, threshold, order);
+    if (i64) return boo_build_t<int64_t, float>(indptr, indices, data, rows, cols, rl, cl, policy, threshold, order);
+    if (f64) return boo_build_t<int32_t, double>(indptr, indices, data, rows, cols, rl, cl, policy, threshold, order);
+    return boo_build_t<int32_t, float>(indptr, indices, data, rows, cols, rl, cl, policy, threshold, order);
+}
+
+// The BOO arrays travel as a dict (the Python object's __dict__ subset).
+template <typename I, typename S>
+struct BooView {
+    I rows, cols, nb, tail_n;
+    const I *row_grp_ptr, *row_ids, *col_grp_ptr, *col_ids, *blk_row_grp, *blk_col_grp, *blk_nz_ptr;
+    const uint8_t* blk_shift;
+    const uint16_t* nz_idx;
+    const S* nz_val;
+    const I *rem_indptr, *rem_col_ind;
+    const S* rem_vals;
+    const I *tail_row, *tail_col;
+    const S* tail_val;
+};
+
+template <typename I, typename S>
+BooView<I, S> boo_view(const py::dict& d) {
+    BooView<I, S> v;
+    v.rows = (I)d["rows"].cast<int64_t>();
+    v.cols = (I)d["cols"].cast<int64_t>();
+    auto arr = [&](const char* k) { return d[k].cast<py::array>(); };
+    v.row_grp_ptr = ptr_of<I>(arr("row_grp_ptr"), "row_grp_ptr");
+    v.row_ids = ptr_of<I>(arr("row_ids"), "row_ids");
+    v.col_grp_ptr = ptr_of<I>(arr("col_grp_ptr"), "col_grp_ptr");
+    v.col_ids = ptr_of<I>(arr("col_ids"), "col_ids");
+    v.blk_row_grp = ptr_of<I>(arr("blk_row_grp"), "blk_row_grp");
+    v.nb = (I)arr("blk_row_grp").size();
+    v.blk_col_grp = ptr_of<I>(arr("blk_col_grp"), "blk_col_grp");
+    v.blk_nz_ptr = ptr_of<I>(arr("blk_nz_ptr"), "blk_nz_ptr");
+    v.blk_shift = ptr_of<uint8_t>(arr("blk_shift"), "blk_shift");
+    v.nz_idx = ptr_of<uint16_t>(arr("nz_idx"), "nz_idx");
+    v.nz_val = ptr_of<S>(arr("nz_val"), "nz_val");
+    v.rem_indptr = ptr_of<I>(arr("rem_indptr"), "rem_indptr");
+    v.rem_col_ind = ptr_of<I>(arr("rem_col_ind"), "rem_col_ind");
+    v.rem_vals = ptr_of<S>(arr("rem_vals"), "rem_vals");
+    v.tail_row = ptr_of<I>(arr("tail_row"), "tail_row");
+    v.tail_col = ptr_of<I>(arr("tail_col"), "tail_col");
+    v.tail_val = ptr_of<S>(arr("tail_val"), "tail_val");
+    v.tail_n = (I)arr("tail_val").size();
+    return v;
+}
+
+template <typename I, typename S>
+void boo_to_csr_t(const py::dict& d, py::array& out_indptr, py::array& out_indices, py::array& out_data) {
+    auto v = boo_view<I, S>(d);
+    I* op = mut_ptr_of<I>(out_indptr, "indptr");
+    I* oi = mut_ptr_of<I>(out_indices, "indices");
+    S* od = mut_ptr_of<S>(out_data, "data");
+    py::gil_scoped_release nogil;
+    spmm::boo_decode<I, S>(v.rows, v.row_grp_ptr, v.row_ids, v.col_grp_ptr, v.col_ids, v.nb,
+                           v.blk_row_grp, v.blk_col_grp, v.blk_nz_ptr, v.blk_shift, v.nz_idx,
+                           v.nz_val, v.rem_indptr, v.rem_col_ind, v.rem_vals, v.tail_n, v.tail_row,
+                           v.tail_col, v.tail_val, op, oi, od);
+}
+
+template <typename I, typename S>
+void boo_matmul_cpu_t(const py::dict& d, const py::array& x, py::array& y, int64_t batch, int64_t K) {
+    auto v = boo_view<I, S>(d);
+    const S* xp = ptr_of<S>(x, "x");
+    S* yp = mut_ptr_of<S>(y, "y");
+    if ((int64_t)x.size() != batch * (int64_t)v.cols * K || (int64_t)y.size() != batch * (int64_t)v.rows * K)
+        throw std::invalid_argument("boo_matmul_cpu: x/y sizes do not match the matrix");
+    py::gil_scoped_release nogil;
+    spmm::boo_matmul_host<I, S>(v.rows, v.cols, v.row_grp_ptr, v.row_ids, v.col_grp_ptr, v.col_ids,
+                                v.nb, v.blk_row_grp, v.blk_col_grp, v.blk_nz_ptr, v.blk_shift,
+                                v.nz_idx, v.nz_val, v.rem_indptr, v.rem_col_ind, v.rem_vals,
+                                v.tail_n, v.tail_row, v.tail_col, v.tail_val, xp, yp, batch, K);
+}
+
+#define SPMM_DISPATCH_IS(i64, f64, FN, ...)                      \
+    do {                                                         \
+        if (i64 && f64) return FN<int64_t, double>(__VA_ARGS__); \
+        if (i64) return FN<int64_t, float>(__VA_ARGS__);         \
+        if (f64) return FN<int32_t, double>(__VA_ARGS__);        \
+        return FN<int32_t, float>(__VA_ARGS__);                  \
+    } while (0)
+
+// ---------------------------------------------------------------- PBR host
+template <typename I, typename S>
+py::dict pbr_build_t(const py::array& indptr, const py::array& indices, const py::array& data,
+                     int64_t rows, int64_t cols, int64_t br, int64_t bc, int min_nnz) {
+    const I* ip = ptr_of<I>(indptr, "indptr");
+    const I* ix = ptr_of<I>(indices, "indices");
+    const S* dv = ptr_of<S>(data, "data");
+    if ((int64_t)indptr.size() != rows + 1)
+        throw std::invalid_argument("csr_to_pbr: indptr must have rows+1 entries");
+    spmm::PbrArrays<I, S> P;
+    {
+        py::gil_scoped_release nogil;
+        P = spmm::build_pbr<I, S>(ip, ix, dv, (I)rows, (I)cols, (I)br, (I)bc, (uint8_t)min_nnz);
+    }
+    py::dict d;
+    d["rows"] = (int64_t)P.rows;
+    d["cols"] = (int64_t)P.cols;
+    d["block_rows"] = (int64_t)P.block_rows;
+    d["block_cols"] = (int64_t)P.block_cols;
+    d["total_nnz"] = (int64_t)P.total_nnz;
+    d["block_codes"] = give(std::move(P.codes));
+    d["block_coords"] = give(std::move(P.coords));
+    d["block_offsets"] = give(std::move(P.offsets));
+    d["block_data"] = give(std::move(P.data));
+    d["remainder_indptr"] = give(std::move(P.rem_indptr));
+    d["remainder_col_ind"] = give(std::move(P.rem_col_ind));
+    d["remainder_data"] = give(std::move(P.rem_vals));
+    return d;
+}
+
+py::dict pbr_build(const py::array& indptr, const py::array& indices, const py::array& data,
+                   int64_t rows, int64_t cols, int64_t br, int64_t bc, int min_nnz) {
+    if (min_nnz < 0 || min_nnz > 255)
+        throw std::invalid_argument("csr_to_pbr: min_nnz_per_block must fit in uint8 (0..255)");
+    SPMM_DISPATCH_IS(is_i64(indptr), is_f64(data), pbr_build_t, indptr, indices, data, rows, cols, br, bc, min_nnz);
+}
+
+template <typename I, typename S>
+int64_t pbr_to_csr_t(const py::dict& d, py::array& out_indptr, py::array& out_indices, py::array& out_data) {
+    auto arr = [&](const char* k) { return d[k].cast<py::array>(); };
+    const I rows = (I)d["rows"].cast<int64_t>(), cols = (I)d["cols"].cast<int64_t>();
+    const I br = (I)d["block_rows"].cast<int64_t>(), bc = (I)d["block_cols"].cast<int64_t>();
+    const py::array codes = arr("block_codes");
+    const uint64_t* cp = ptr_of<uint64_t>(codes, "block_codes");
+    const I* co = ptr_of<I>(arr("block_coords"), "block_coords");
+    const S* dp = ptr_of<S>(arr("block_data"), "block_data");
+    const I* ri = ptr_of<I>(arr("remainder_indptr"), "remainder_indptr");
+    const I* rc = ptr_of<I>(arr("remainder_col_ind"), "remainder_col_ind");
+    const S* rv = ptr_of<S>(arr("remainder_data"), "remainder_data");
+    I* op = mut_ptr_of<I>(out_indptr, "indptr");
+    I* oi = mut_ptr_of<I>(out_indices, "indices");
+    S* od = mut_ptr_of<S>(out_data, "data");
+    py::gil_scoped_release nogil;
+    return (int64_t)spmm::pbr_decode<I, S>(rows, cols, br, bc, (size_t)codes.size(), cp, co, dp, ri, rc,
+                                           rv, op, oi, od);
+}
+
+template <typename I, typename S>
+void pbr_matmul_cpu_t(const py::dict& d, const py::array& x, py::array& y, int64_t batch, int64_t K) {
+    auto arr = [&](const char* k) { return d[k].cast<py::array>(); };
+    const I rows = (I)d["rows"].cast<int64_t>(), cols = (I)d["cols"].cast<int64_t>();
+    const I br = (I)d["block_rows"].cast<int64_t>(), bc = (I)d["block_cols"].cast<int64_t>();
+    const py::array codes = arr("block_codes");
+    const uint64_t* cp = ptr_of<uint64_t>(codes, "block_codes");
+    const I* co = ptr_of<I>(arr("block_coords"), "block_coords");
+    const S* dp = ptr_of<S>(arr("block_data"), "block_data");
+    const I* ri = ptr_of<I>(arr("remainder_indptr"), "remainder_indptr");
+    const I* rc = ptr_of<I>(arr("remainder_col_ind"), "remainder_col_ind");
+    const S* rv = ptr_of<S>(arr("remainder_data"), "remainder_data");
+    const S* xp = ptr_of<S>(x, "x");
+    S* yp = mut_ptr_of<S>(y, "y");
+    if ((int64_t)x.size() != batch * (int64_t)cols * K || (int64_t)y.size() != batch * (int64_t)rows * K)
+        throw std::invalid_argument("pbr_matmul_cpu: x/y sizes do not match the matrix");
+    py::gil_scoped_release nogil;
+    spmm::pbr_matmul_host<I, S>(rows, cols, br, bc, (size_t)codes.size(), cp, co, dp, ri, rc, rv, xp,
+                                yp, batch, K);
+}
+
+// ---------------------------------------------------------------- GPU glue
+uintptr_t P(const py::dict& d, const char* k) { return d[k].cast<uintptr_t>(); }
+
+spmm_boo_desc boo_desc(const py::dict& d) {
+    spmm_boo_desc A{};
+    A.rows = d["rows"].cast<int32_t>();
+    A.cols = d["cols"].cast<int32_t>();
+    A.n_row_groups = d["n_row_groups"].cast<int32_t>();
+    A.n_col_groups = d["n_col_groups"].cast<int32_t>();
+    A.num_blocks = d["num_blocks"].cast<int32_t>();
+    A.max_nr = d["max_nr"].cast<int32_t>();
+    A.max_nc = d["max_nc"].cast<int32_t>();
+    A.max_nnz_blk = d["max_nnz_blk"].cast<int32_t>();
+    A.row_grp_ptr = reinterpret_cast<const int32_t*>(P(d, "row_grp_ptr"));
+    A.row_ids = reinterpret_cast<const int32_t*>(P(d, "row_ids"));
+    A.col_grp_ptr = reinterpret_cast<const int32_t*>(P(d, "col_grp_ptr"));
+    A.col_ids = reinterpret_cast<const int32_t*>(P(d, "col_ids"));
+    A.blk_col_grp = reinterpret_cast<const int32_t*>(P(d, "blk_col_grp"));
+    A.blk_nz_ptr = reinterpret_cast<const int32_t*>(P(d, "blk_nz_ptr"));
+    A.blk_shift = reinterpret_cast<const uint8_t*>(P(d, "blk_shift"));
+    A.nz_idx = reinterpret_cast<const uint16_t*>(P(d, "nz_idx"));
+    A.nz_val = reinterpret_cast<const void*>(P(d, "nz_val"));
+    A.rem_indptr = reinterpret_cast<const int32_t*>(P(d, "rem_indptr"));
+    A.rem_col_ind = reinterpret_cast<const int32_t*>(P(d, "rem_col_ind"));
+    A.rem_vals = reinterpret_cast<const void*>(P(d, "rem_vals"));
+    A.n_items = d["n_items"].cast<int32_t>();
+    A.items = reinterpret_cast<const int32_t*>(P(d, "items"));
+    A.n_slots = d["n_slots"].cast<int32_t>();
+    A.n_splits = d["n_splits"].cast<int32_t>();
+    A.splits = reinterpret_cast<const int32_t*>(P(d, "splits"));
+    A.n_long = d["n_long"].cast<int32_t>();
+    A.long_rows = reinterpret_cast<const int32_t*>(P(d, "long_rows"));
+    A.long_threshold = d["long_threshold"].cast<int32_t>();
+    return A;
+}
+
+py::dict boo_plan(int32_t rows, int32_t n_rg, const py::array& row_grp_ptr, const py::array& blk_row_grp,
+                  const py::array& blk_nz_ptr, const py::array& rem_indptr, int32_t max_item_nnz,
+                  int32_t long_threshold) {
+    const int32_t* rgp = ptr_of<int32_t>(row_grp_ptr, "row_grp_ptr");
+    const int32_t* brg = ptr_of<int32_t>(blk_row_grp, "blk_row_grp");
+    const int32_t* bnp = ptr_of<int32_t>(blk_nz_ptr, "blk_nz_ptr");
+    const int32_t* rip = ptr_of<int32_t>(rem_indptr, "rem_indptr");
+    const int32_t nb = (int32_t)blk_row_grp.size();
+    int32_t n_items = 0, n_slots = 0, n_splits = 0, n_long = 0;
+    raise_status(spmm_boo_plan_build(rows, n_rg, nb, rgp, brg, bnp, rip, max_item_nnz, long_threshold,
+                                     nullptr, nullptr, 0, nullptr, &n_items, &n_slots, &n_splits, &n_long));
+    std::vector<int32_t> items((size_t)n_items * 4), splits((size_t)n_items * 3), longr((size_t)rows);
+    raise_status(spmm_boo_plan_build(rows, n_rg, nb, rgp, brg, bnp, rip, max_item_nnz, long_threshold,
+                                     items.data(), splits.data(), n_items, longr.data(), &n_items,
+                                     &n_slots, &n_splits, &n_long));
+    splits.resize((size_t)n_splits * 3);
+    longr.resize((size_t)n_long);
+    py::dict d;
+    d["items"] = give(std::move(items));
+    d["splits"] = give(std::move(splits));
+    d["long_rows"] = give(std::move(longr));
+    d["n_items"] = n_items;
+    d["n_slots"] = n_slots;
+    d["n_splits"] = n_splits;
+    d["n_long"] = n_long;
+    return d;
+}
+
+size_t boo_workspace_bytes(const py::dict& d, int dtype, int64_t batch, int64_t K) {
+    spmm_boo_desc A = boo_desc(d);
+    return spmm_boo_workspace_bytes(&A, (spmm_dtype)dtype, batch, K);
+}
+
+void boo_matmul_gpu(const py::dict& d, int dtype, uintptr_t x, uintptr_t y, int64_t batch, int64_t K,
+                    uintptr_t ws, size_t ws_bytes, uintptr_t stream) {
+    spmm_boo_desc A = boo_desc(d);
+    raise_status(spmm_boo_matmul(&A, (spmm_dtype)dtype, reinterpret_cast<const void*>(x),
+                                 reinterpret_cast<void*>(y), batch, K, reinterpret_cast<void*>(ws),
+                                 ws_bytes, reinterpret_cast<void*>(stream)));
+}
+
+void pbr_matmul_gpu(const py::dict& d, int dtype, uintptr_t x, uintptr_t y, int64_t batch, int64_t K,
+                    uintptr_t stream) {
+    spmm_pbr_desc A{};
+    A.rows = d["rows"].cast<int64_t>();
+    A.cols = d["cols"].cast<int64_t>();
+    A.block_rows = d["block_rows"].cast<int32_t>();
+    A.block_cols = d["block_cols"].cast<int32_t>();
+    A.num_blocks = d["num_blocks"].cast<int64_t>();
+    A.itype = (spmm_itype)d["itype"].cast<int>();
+    A.codes = reinterpret_cast<const int64_t*>(P(d, "codes"));
+    A.coords = reinterpret_cast<const void*>(P(d, "coords"));
+    A.offsets = reinterpret_cast<const void*>(P(d, "offsets"));
+    A.data = reinterpret_cast<const void*>(P(d, "data"));
+    A.rem_indptr = reinterpret_cast<const void*>(P(d, "rem_indptr"));
+    A.rem_col_ind = reinterpret_cast<const void*>(P(d, "rem_col_ind"));
+    A.rem_vals = reinterpret_cast<const void*>(P(d, "rem_vals"));
+    A.stripe_ptr = reinterpret_cast<const int32_t*>(P(d, "stripe_ptr"));
+    A.n_long = d["n_long"].cast<int32_t>();
+    A.long_rows = reinterpret_cast<const int32_t*>(P(d, "long_rows"));
+    A.long_threshold = d["long_threshold"].cast<int32_t>();
+    raise_status(spmm_pbr_matmul(&A, (spmm_dtype)dtype, reinterpret_cast<const void*>(x),
+                                 reinterpret_cast<void*>(y), batch, K, reinterpret_cast<void*>(stream)));
+}
+
+void csr_naive_gpu(uintptr_t indptr, uintptr_t col, uintptr_t vals, int itype, int dtype, int64_t rows,
+                   int64_t cols, uintptr_t x, uintptr_t y, int64_t K, uintptr_t stream) {
+    raise_status(spmm_csr_naive(reinterpret_cast<const void*>(indptr), reinterpret_cast<const void*>(col),
+                                reinterpret_cast<const void*>(vals), (spmm_itype)itype, (spmm_dtype)dtype,
+                                rows, cols, reinterpret_cast<const void*>(x), reinterpret_cast<void*>(y), K,
+                                reinterpret_cast<void*>(stream)));
+}
+
+}  // namespace
+
+PYBIND11_MODULE(_core, m) {
+    m.doc() = "spmm_amd native host layer (format builders, CPU ops, C-ABI GPU glue)";
+    m.def("csr_to_boo", &boo_build);
+    m.def("boo_to_csr", [](const py::dict& d, py::array& ip, py::array& ix, py::array& dv) {
+        SPMM_DISPATCH_IS(is_i64(ip), is_f64(dv), boo_to_csr_t, d, ip, ix, dv);
+    });
+    m.def("boo_matmul_cpu", [](const py::dict& d, const py::array& x, py::array& y, int64_t batch, int64_t K) {
+        SPMM_DISPATCH_IS(is_i64(d["row_ids"].cast<py::array>()), is_f64(x), boo_matmul_cpu_t, d, x, y, batch, K);
+    });
+    m.def("csr_to_pbr", &pbr_build);
+    m.def("pbr_to_csr", [](const py::dict& d, py::array& ip, py::array& ix, py::array& dv) -> int64_t {
+        SPMM_DISPATCH_IS(is_i64(ip), is_f64(dv), pbr_to_csr_t, d, ip, ix, dv);
+    });
+    m.def("pbr_matmul_cpu", [](const py::dict& d, const py::array& x, py::array& y, int64_t batch, int64_t K) {
+        SPMM_DISPATCH_IS(is_i64(d["block_offsets"].cast<py::array>()), is_f64(x), pbr_matmul_cpu_t, d, x, y,
+                         batch, K);
+    });
+    m.def("boo_plan", &boo_plan);
+    m.def("boo_workspace_bytes", &boo_workspace_bytes);
+    m.def("boo_matmul_gpu", &boo_matmul_gpu);
+    m.def("pbr_matmul_gpu", &pbr_matmul_gpu);
+    m.def("csr_naive_gpu", &csr_naive_gpu);
+    m.def("version", []() { return std::string(spmm_version()); });
+}
