@@ -1,0 +1,252 @@
+"""SpMM benchmark: boo_matmul on the 3-D 27-point stencil (64^3, K=64, fp32).
+
+Metric: SpMM GFLOP/s = 2*nnz*K/t, with the achieved HBM GB/s
+of the algorithmic bytes 4(2nnz + m + 1) + 4K(x_rows + m) against MI355X's
+8 TB/s.  One step = one boo_matmul of the whole matrix against one X.
+
+Inputs are resident in HBM before timing starts, and the timed loop rotates
+over NROT independent copies (matrix staging, X, Y) whose combined size is
+well beyond the 256 MB Infinity Cache, so a step cannot be served from the
+previous step's cached data.  Steps are issued through the C ABI with
+preallocated outputs (the reference's timed-harness scope,
+bindings/bindings_boo_timed.cu); the Python-API cost per call is reported
+beside it.
+
+Output: one JSON line on stdout (rank 0), as the driver expects.
+    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--config 2]
+    python bench.py --calibrate-copy   # plain copy of known size, for rocprof scaling
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+PEAK_HBM_GBS = 8000.0
+NROT = 4
+
+
+def _log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def bytes_alg(A, K):
+    """4(2 nnz + m + 1) + 4K(x_rows_referenced + m): fp32 values, int32
+    indices (reports/agent_loop/BENCH_SCHEMA.md:104 of the reference)."""
+    m = A.shape[0]
+    x_rows = int(np.unique(A.indices).size)
+    return 4 * (2 * A.nnz + m + 1) + 4 * K * (x_rows + m)
+
+
+def time_steps(fns, steps, warmup, torch):
+    """Wall time of exactly `steps` calls (rotating over fns), bracketed by
+    synchronize on both sides, and the per-call GPU time from events on the
+    stream the kernels run on."""
+    for i in range(warmup):
+        fns[i % len(fns)]()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev[i][0].record(stream)
+        fns[i % len(fns)]()
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = sorted(a.elapsed_time(b) for a, b in ev)      # ms
+    return wall / steps * 1e3, sum(per) / len(per), per[len(per) // 2]
+
+
+def cpu_baseline(A, spec):
+    """The reference's own CPU BOO op (boo_batched_matmul_cpu, single thread),
+    compiled from its sources into oracle/_ref, on the same config."""
+    import importlib
+    import torch
+    ref_dir = ROOT / 'oracle' / '_ref'
+    if not any(ref_dir.glob('torch_fast_spdmm_core*.so')):
+        return None
+    sys.path.insert(0, str(ref_dir))
+    ref = importlib.import_module('torch_fast_spdmm_core')
+    sys.path.insert(0, str(ROOT))
+    from oracle import oracle as O
+    K = spec['K']
+    rl = O.identity_labels(A.shape[0], 32)
+    b = ref.csr_to_boo(A.indptr, A.indices, A.data, A.shape[0], A.shape[1], rl, rl, 2, 4, 0)
+    from spmm_amd import matrices as M
+    x = torch.from_numpy(M.dense_x(A.shape[1], K))
+    nthreads = torch.get_num_threads()
+    torch.set_num_threads(1)
+    try:
+        ref.boo_batched_matmul_cpu(b, x)                    # warmup
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            ref.boo_batched_matmul_cpu(b, x)
+            ts.append(time.perf_counter() - t0)
+    finally:
+        torch.set_num_threads(nthreads)
+    t = sorted(ts)[1]
+    cpu_model = platform.processor() or 'x86_64'
+    try:
+        with open('/proc/cpuinfo') as f:
+            for line in f:
+                if line.startswith('model name'):
+                    cpu_model = line.split(':', 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {'value': round(2.0 * A.nnz * K / t / 1e9, 3), 'unit': 'GFLOP/s', 'cores': 1,
+            'kind': 'reference',
+            'sample': f'full config-2 matrix, K={K}: boo_batched_matmul_cpu, 1 warmup + median of 3 '
+                      f'({t * 1e3:.0f} ms/call), single thread',
+            'host_cpu': cpu_model, 'host_cores_available': len(os.sched_getaffinity(0))}
+
+
+def traffic_from_profiles(workload):
+    p = ROOT / 'profiles' / f'{workload}_traffic.json'
+    if p.exists():
+        try:
+            return json.loads(p.read_text())
+        except ValueError:
+            return None
+    return None
+
+
+def calibrate_copy(torch):
+    """A plain device copy of known size, for scaling FETCH_SIZE/WRITE_SIZE."""
+    n = 128 * 1024 * 1024                                   # 512 MiB of fp32
+    a = torch.ones(n, device='cuda')
+    b = torch.empty_like(a)
+    for _ in range(5):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({'calibrate_copy_bytes_each_way': 4 * n, 'reps': 5}))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=50)
+    ap.add_argument('--warmup', type=int, default=10)
+    ap.add_argument('--config', type=int, default=2)
+    ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--calibrate-copy', action='store_true')
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
+        print(f'bench.py: this build measures one GPU only (the SpMM path has no multi-GPU '
+              f'component); got --gpus {args.gpus}', file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    sys.path.insert(0, str(ROOT))
+    import spmm_amd as S
+    from spmm_amd import matrices as M
+
+    if args.calibrate_copy:
+        calibrate_copy(torch)
+        return
+
+    A, spec = M.make_config(args.config)
+    K = spec['K']
+    nnz, m = A.nnz, A.shape[0]
+    balg = bytes_alg(A, K)
+    flops = 2.0 * nnz * K
+    _log(f'config {args.config}: {spec["name"]} {A.shape} nnz={nnz} K={K} bytes_alg={balg}')
+
+    out = {}
+    Xs = [torch.from_numpy(M.dense_x(A.shape[1], K, seed=s)).cuda() for s in range(NROT)]
+    dev = torch.device('cuda', torch.cuda.current_device())
+
+    # ---- BOO (headline)
+    boos = [S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32).to(dev) for _ in range(NROT)]
+    Ys = [torch.empty((1, m, K), device=dev) for _ in range(NROT)]
+    ws_bytes = int(S._core.boo_workspace_bytes(boos[0]._gpu_meta.desc, 0, 1, K))
+    wss = [torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) for _ in range(NROT)]
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def boo_step(i):
+        S._core.boo_matmul_gpu(boos[i]._gpu_meta.desc, 0, int(Xs[i].data_ptr()), int(Ys[i].data_ptr()),
+                               1, K, int(wss[i].data_ptr()), ws_bytes, int(stream))
+    boo_fns = [lambda i=i: boo_step(i) for i in range(NROT)]
+    # parity of the timed entry point against the fp64 product before timing
+    boo_step(0)
+    torch.cuda.synchronize()
+    from oracle import oracle as O
+    ratio, ok = O.within_bound(Ys[0][0].cpu().numpy(), A, Xs[0].cpu().numpy(), 1e-5)
+    if not ok:
+        _log(f'PARITY FAILURE: max |err|/(|A||X|) = {ratio:.3e}')
+        sys.exit(1)
+    ms_wall, ms_ev_mean, ms_ev_med = time_steps(boo_fns, args.steps, args.warmup, torch)
+    api_fns = [lambda i=i: S.boo_matmul(boos[i], Xs[i]) for i in range(NROT)]
+    ms_api, _, _ = time_steps(api_fns, min(args.steps, 20), 3, torch)
+    _log(f'BOO: wall {ms_wall * 1e3:.1f} us/step, kernel events mean {ms_ev_mean * 1e3:.1f} us '
+         f'median {ms_ev_med * 1e3:.1f} us; python API {ms_api * 1e3:.1f} us/call; '
+         f'parity ratio {ratio:.2e}')
+    gbs = balg / (ms_ev_mean * 1e-3) / 1e9
+
+    # ---- PBR on the same matrix
+    pbr = {}
+    if 'pbr' in spec['formats']:
+        thr = spec.get('pbr_threshold', 4)
+        pbrs = [S.csr_to_pbr(A, 8, 8, thr).to(dev) for _ in range(NROT)]
+
+        def pbr_step(i):
+            S._core.pbr_matmul_gpu(pbrs[i]._gpu_meta.desc, 0, int(Xs[i].data_ptr()),
+                                   int(Ys[i].data_ptr()), 1, K, int(stream))
+        pbr_step(0)
+        torch.cuda.synchronize()
+        pratio, pok = O.within_bound(Ys[0][0].cpu().numpy(), A, Xs[0].cpu().numpy(), 1e-5)
+        if not pok:
+            _log(f'PBR PARITY FAILURE: {pratio:.3e}')
+            sys.exit(1)
+        p_wall, p_ev, _ = time_steps([lambda i=i: pbr_step(i) for i in range(NROT)], args.steps,
+                                     args.warmup, torch)
+        pbr = {'ms_per_step': round(p_wall, 5), 'kernel_ms_mean': round(p_ev, 5),
+               'gflops': round(flops / (p_wall * 1e-3) / 1e9, 2),
+               'hbm_gbs': round(balg / (p_ev * 1e-3) / 1e9, 1),
+               'hbm_frac': round(balg / (p_ev * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+        _log(f'PBR: wall {p_wall * 1e3:.1f} us/step, kernel {p_ev * 1e3:.1f} us')
+
+    workload = f'cfg{args.config}_{spec["name"]}_boo_identity32_K{K}'
+    cpu = None if args.no_cpu_baseline else cpu_baseline(A, spec)
+    out = {
+        'metric': 'SpMM GFLOP/s (2*nnz*K/t), boo_matmul; HBM GB/s of algorithmic bytes vs 8 TB/s',
+        'value': round(flops / (ms_wall * 1e-3) / 1e9, 2),
+        'unit': 'GFLOP/s',
+        'n_gpus': 1,
+        'steps': args.steps,
+        'warmup': args.warmup,
+        'ms_per_step': round(ms_wall, 5),
+        'higher_is_better': True,
+        'scaling': 'weak',
+        'vs_baseline': None,
+        'dtype': 'f32',
+        'data': 'synthetic',
+        'config': {'workload': workload, 'matrix': spec['name'], 'rows': m, 'nnz': nnz, 'K': K,
+                   'format': 'BOO identity 32x32, remainder policy (threshold 4)',
+                   'bytes_alg': balg, 'rotation_copies': NROT},
+        'hbm_gbs': round(balg / (ms_wall * 1e-3) / 1e9, 1),
+        'roofline': {'bound': 'hbm', 'achieved': round(gbs, 1), 'peak': PEAK_HBM_GBS, 'unit': 'GB/s',
+                     'frac': round(gbs / PEAK_HBM_GBS, 4),
+                     'traffic': (traffic_from_profiles(workload) or {}).get('bytes_per_launch')},
+        'kernel_us_mean': round(ms_ev_mean * 1e3, 2),
+        'python_api_us_per_call': round(ms_api * 1e3, 2),
+        'pbr': pbr,
+        'cpu_baseline': cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == '__main__':
+    main()
