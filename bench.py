@@ -15,6 +15,7 @@ beside it.
 Output: one JSON line on stdout (rank 0), as the driver expects.
     python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--config 2]
     python bench.py --calibrate-copy   # plain copy of known size, for rocprof scaling
+    python bench.py --steps 5 --warmup 2 --no-pbr --no-cpu-baseline   # BOO only (counter runs)
 """
 
 from __future__ import annotations
@@ -47,24 +48,23 @@ def bytes_alg(A, K):
 
 
 def time_steps(fns, steps, warmup, torch):
-    """Wall time of exactly `steps` calls (rotating over fns), bracketed by
-    synchronize on both sides, and the per-call GPU time from events on the
-    stream the kernels run on."""
+    """Exactly `steps` calls (rotating over fns), bracketed by synchronize on
+    both sides.  Returns (wall ms per step, GPU ms per step): the second is
+    one HIP event pair on the launch stream around the whole timed region,
+    divided by the step count, so no per-step marker sits between kernels."""
     for i in range(warmup):
         fns[i % len(fns)]()
-    torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(steps)]
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
+    e0.record(stream)
     for i in range(steps):
-        ev[i][0].record(stream)
         fns[i % len(fns)]()
-        ev[i][1].record(stream)
+    e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    per = sorted(a.elapsed_time(b) for a, b in ev)      # ms
-    return wall / steps * 1e3, sum(per) / len(per), per[len(per) // 2]
+    return wall / steps * 1e3, e0.elapsed_time(e1) / steps
 
 
 def cpu_baseline(A, spec):
@@ -140,6 +140,7 @@ def main():
     ap.add_argument('--warmup', type=int, default=10)
     ap.add_argument('--config', type=int, default=2)
     ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--no-pbr', action='store_true', help='skip the PBR line (profiling runs)')
     ap.add_argument('--calibrate-copy', action='store_true')
     args = ap.parse_args()
 
@@ -187,17 +188,17 @@ def main():
     if not ok:
         _log(f'PARITY FAILURE: max |err|/(|A||X|) = {ratio:.3e}')
         sys.exit(1)
-    ms_wall, ms_ev_mean, ms_ev_med = time_steps(boo_fns, args.steps, args.warmup, torch)
+    ms_wall, ms_ev_mean = time_steps(boo_fns, args.steps, args.warmup, torch)
     api_fns = [lambda i=i: S.boo_matmul(boos[i], Xs[i]) for i in range(NROT)]
-    ms_api, _, _ = time_steps(api_fns, min(args.steps, 20), 3, torch)
-    _log(f'BOO: wall {ms_wall * 1e3:.1f} us/step, kernel events mean {ms_ev_mean * 1e3:.1f} us '
-         f'median {ms_ev_med * 1e3:.1f} us; python API {ms_api * 1e3:.1f} us/call; '
+    ms_api, _ = time_steps(api_fns, min(args.steps, 20), 3, torch)
+    _log(f'BOO: wall {ms_wall * 1e3:.1f} us/step, GPU (events over the timed region) '
+         f'{ms_ev_mean * 1e3:.1f} us/step; python API {ms_api * 1e3:.1f} us/call; '
          f'parity ratio {ratio:.2e}')
     gbs = balg / (ms_ev_mean * 1e-3) / 1e9
 
     # ---- PBR on the same matrix
     pbr = {}
-    if 'pbr' in spec['formats']:
+    if 'pbr' in spec['formats'] and not args.no_pbr:
         thr = spec.get('pbr_threshold', 4)
         pbrs = [S.csr_to_pbr(A, 8, 8, thr).to(dev) for _ in range(NROT)]
 
@@ -210,7 +211,7 @@ def main():
         if not pok:
             _log(f'PBR PARITY FAILURE: {pratio:.3e}')
             sys.exit(1)
-        p_wall, p_ev, _ = time_steps([lambda i=i: pbr_step(i) for i in range(NROT)], args.steps,
+        p_wall, p_ev = time_steps([lambda i=i: pbr_step(i) for i in range(NROT)], args.steps,
                                      args.warmup, torch)
         pbr = {'ms_per_step': round(p_wall, 5), 'kernel_ms_mean': round(p_ev, 5),
                'gflops': round(flops / (p_wall * 1e-3) / 1e9, 2),
