@@ -24,10 +24,11 @@
  *                         (bindings/bindings_kernels.cu:91-123, 18-89, 436-439)
  *                         + launch_pbr_spmm (kernels/pbr_kernel.cu:329-390)
  *   spmm_csr_naive     <- spdmm_csr_naive (kernels/csr_kernels.cu:31-53)
- *   spmm_boo_plan_*    <- no single counterpart: the row-group schedule the
- *                         reference never builds because it launches one CTA
- *                         per block and resolves rows with atomics
- *                         (kernels/boo_kernel.cu:574-590).
+ *   spmm_boo_stage_*   <- the staging of _boo_to_method (torch_fast_spdmm/boo.py:54-96)
+ *                         and prepare_boo_cuda's precomputed row tables
+ *                         (torch_fast_spdmm/boo_plan.py:84-123); the tile stream
+ *                         replaces the reference's one-CTA-per-block launch with
+ *                         row merging by atomics (kernels/boo_kernel.cu:574-590).
  */
 #ifndef SPMM_AMD_H_
 #define SPMM_AMD_H_
@@ -57,68 +58,102 @@ const char* spmm_last_error(void);
 const char* spmm_version(void);
 
 /* ---------------------------------------------------------------------------
- * BOO (blocked COO).  Arrays are exactly those csr_to_boo emits
- * (boo_matrix/boo_matrix.hpp:56-138) narrowed to int32, with nz_idx sorted
- * row-major inside every block (nz_order == rowmajor; the host stages a
- * row-major copy for column-major matrices).  The tail of the tail_batch
- * policy is passed merged into the remainder CSR (rem_*), so every row's
- * non-block entries are one CSR row.
+ * BOO (blocked COO).
  *
- * The schedule (work items) comes from spmm_boo_plan_build: one item is one
- * row group, or a contiguous slice of a heavy row group's blocks.  The first
- * item of a row group (slot < 0) owns its rows: it adds the remainder and
- * stores Y directly.  The other items of a split row group write partial sums
- * to workspace slots, and a second pass adds them into Y in slot order, so the
- * result does not depend on scheduling.  Remainder rows longer than
- * long_threshold are left out of the owner item and summed by a split-row pass
- * that runs last.
+ * The device-side BOO operand is a tile stream staged once on the host from
+ * the arrays csr_to_boo emits (boo_matrix/boo_matrix.hpp:56-138; the
+ * reference stages its own GPU copy in torch_fast_spdmm/boo.py:54-96 and,
+ * for its plan mode, precomputed row tables in boo_plan.py:84-123):
+ *
+ *   spmm_boo_stage_create   host BOO arrays -> opaque staging (host memory)
+ *   spmm_boo_stage_sizes    array lengths, so the caller can allocate
+ *   spmm_boo_stage_copy     copy the arrays out (host pointers)
+ *   spmm_boo_stage_destroy
+ *
+ * The caller copies the arrays to the device and fills spmm_boo_desc.
+ * Every row group is cut into 32-row slices; each slice's work becomes tiles
+ * of <= 32 rows x <= 32 columns with <= 128 entries (block entries keep the
+ * block's row-major order; the slice's remainder rows with <= long_threshold
+ * entries become tiles over their distinct columns; longer remainder rows are
+ * listed in long_rows and summed by a split-row pass).  A slice heavier than
+ * max_item_nnz is cut into several items: the first stores Y, the others
+ * write partial sums to workspace slots that a fixup pass adds in slot order,
+ * so results do not depend on scheduling.  Items are dealt to n_waves
+ * persistent waves as contiguous ranges of near-equal cost.
  * ------------------------------------------------------------------------- */
+
+/* Host copies of csr_to_boo's arrays, int32 indices, nz_idx row-major inside
+ * every block (a column-major matrix needs a row-major copy). */
+typedef struct spmm_boo_host {
+    int32_t rows, cols, n_row_groups, n_col_groups, num_blocks;
+    spmm_dtype dtype;
+    const int32_t* row_grp_ptr;  /* [n_row_groups+1] */
+    const int32_t* row_ids;      /* [rows] */
+    const int32_t* col_grp_ptr;  /* [n_col_groups+1] */
+    const int32_t* col_ids;      /* [cols] */
+    const int32_t* blk_row_grp;  /* [num_blocks], nondecreasing */
+    const int32_t* blk_col_grp;  /* [num_blocks] */
+    const int32_t* blk_nz_ptr;   /* [num_blocks+1] */
+    const uint8_t* blk_shift;    /* [num_blocks] */
+    const uint16_t* nz_idx;      /* [compressed_nnz] */
+    const void* nz_val;          /* [compressed_nnz] float or double */
+    const int32_t* rem_indptr;   /* [rows+1]; the tail, if any, merged in */
+    const int32_t* rem_col_ind;
+    const void* rem_vals;
+} spmm_boo_host;
+
+typedef struct spmm_boo_stage spmm_boo_stage;  /* opaque, host memory */
+
+typedef struct spmm_boo_stage_info {
+    int64_t n_tiles, n_ent, n_tcols, n_splits, n_long;
+    int32_t n_slots, n_waves, group;
+} spmm_boo_stage_info;
+
+/* group (1, 2 or 4): slices that share column chunks are put together, up to
+ * group of them, and walk one tile stream in lockstep -- the waves of one
+ * workgroup, each owning one slice, load each X tile once between them.
+ * n_waves is rounded down to a multiple of group. */
+int spmm_boo_stage_create(const spmm_boo_host* H, int32_t max_item_nnz, int32_t long_threshold,
+                          int32_t n_waves, int32_t group, spmm_boo_stage** out);
+int spmm_boo_stage_sizes(const spmm_boo_stage* st, spmm_boo_stage_info* info);
+/* Host output arrays, sized from spmm_boo_stage_sizes:
+ *   tiles [n_tiles*8] int32: ent_off, nnz | nc<<8 | nr<<16 | flags<<24, cid_off, row_off,
+ *                            slot (-1: the item stores Y, else its partial slot), 0, 0, 0
+ *   tile_rs [n_tiles*33] uint16, ent_val [n_ent] (dtype), ent_col [n_ent] uint8,
+ *   tcols [n_tcols] int32, splits [n_splits*4] int32, long_rows [n_long] int32,
+ *   wave_tiles [n_waves+1] int32.
+ * Every tile's entries start at an even index (odd tiles are followed by a
+ * zero entry). */
+int spmm_boo_stage_copy(const spmm_boo_stage* st, int32_t* tiles, uint16_t* tile_rs,
+                        void* ent_val, uint8_t* ent_col, int32_t* tcols, int32_t* splits,
+                        int32_t* long_rows, int32_t* wave_tiles);
+void spmm_boo_stage_destroy(spmm_boo_stage* st);
+
+/* Device descriptor: the staged arrays plus row_ids and the remainder CSR
+ * (read only for long_rows). */
 typedef struct spmm_boo_desc {
     int32_t rows, cols;
-    int32_t n_row_groups, n_col_groups, num_blocks;
-    int32_t max_nr, max_nc, max_nnz_blk;
-    const int32_t* row_grp_ptr; /* [n_row_groups+1] */
-    const int32_t* row_ids;     /* [rows] */
-    const int32_t* col_grp_ptr; /* [n_col_groups+1] */
-    const int32_t* col_ids;     /* [cols] */
-    const int32_t* blk_col_grp; /* [num_blocks] */
-    const int32_t* blk_nz_ptr;  /* [num_blocks+1] */
-    const uint8_t* blk_shift;   /* [num_blocks] */
-    const uint16_t* nz_idx;     /* [compressed_nnz], row-major per block */
-    const void* nz_val;         /* [compressed_nnz] float or double */
-    const int32_t* rem_indptr;  /* [rows+1] */
-    const int32_t* rem_col_ind; /* [remainder_nnz] */
-    const void* rem_vals;       /* [remainder_nnz] */
-    /* schedule from spmm_boo_plan_build, copied to the device */
-    int32_t n_items;
-    const int32_t* items;       /* [n_items*4]: row_group, blk_begin, blk_end, slot */
-    int32_t n_slots;            /* partial-sum slots (0 when no row group is split) */
-    int32_t n_splits;           /* row groups split over more than one item */
-    const int32_t* splits;      /* [n_splits*3]: row_group, slot_begin, slot_end */
-    int32_t n_long;             /* rows whose remainder is longer than long_threshold */
-    const int32_t* long_rows;   /* [n_long] */
-    int32_t long_threshold;
+    const int32_t* row_ids;      /* [rows] */
+    int32_t n_tiles;
+    const int32_t* tiles;        /* [n_tiles*8] */
+    const uint16_t* tile_rs;     /* [n_tiles*33] */
+    const void* ent_val;         /* [n_ent] */
+    const uint8_t* ent_col;      /* [n_ent] */
+    const int32_t* tcols;        /* [n_tcols] */
+    int32_t n_waves;             /* a multiple of group */
+    int32_t group;               /* waves per workgroup walking one stream in lockstep */
+    const int32_t* wave_tiles;   /* [n_waves+1]: equal lengths within each group of waves */
+    int32_t n_slots;             /* partial-sum slots (0 when no slice is split) */
+    int32_t n_splits;
+    const int32_t* splits;       /* [n_splits*4]: row_off, nr, slot_begin, slot_end */
+    int32_t n_long;
+    const int32_t* long_rows;    /* [n_long] */
+    const int32_t* rem_indptr;   /* [rows+1] */
+    const int32_t* rem_col_ind;
+    const void* rem_vals;
 } spmm_boo_desc;
 
-/* Host-side schedule builder (no device work).  Reads host copies of
- * row_grp_ptr, blk_row_grp (blocks sorted by row group, as csr_to_boo emits
- * them), blk_nz_ptr and rem_indptr.  Writes h_items (capacity item_cap*4
- * ints), h_splits (capacity item_cap*3 ints) and h_long_rows (capacity rows),
- * and the counts through n_items/n_slots/n_splits/n_long.  A row group whose
- * blocks hold more than max_item_nnz nonzeros, or that has more than 64
- * blocks, is cut at block boundaries into items within both limits (an item
- * always holds at least one block).  Call with h_items == NULL first: only n_items is
- * computed, and item_cap must then be at least that. */
-int spmm_boo_plan_build(int32_t rows, int32_t n_row_groups, int32_t num_blocks,
-                        const int32_t* h_row_grp_ptr, const int32_t* h_blk_row_grp,
-                        const int32_t* h_blk_nz_ptr, const int32_t* h_rem_indptr,
-                        int32_t max_item_nnz, int32_t long_threshold,
-                        int32_t* h_items, int32_t* h_splits, int32_t item_cap,
-                        int32_t* h_long_rows,
-                        int32_t* n_items, int32_t* n_slots, int32_t* n_splits,
-                        int32_t* n_long);
-
-/* Workspace bytes spmm_boo_matmul needs for this schedule and shape. */
+/* Workspace bytes spmm_boo_matmul needs for this staging and shape. */
 size_t spmm_boo_workspace_bytes(const spmm_boo_desc* A, spmm_dtype dtype, int64_t batch, int64_t K);
 
 /* Y[b] = A X[b] for b < batch.  X: [batch][A->cols][K], Y: [batch][A->rows][K].

@@ -37,9 +37,11 @@ NZ_ORDERS = ('rowmajor', 'colmajor')
 _POLICY_CODE = {'keep': 0, 'merge': 1, 'remainder': 2, 'tail_batch': 3}
 _ORDER_CODE = {'rowmajor': 0, 'colmajor': 1}
 
-# Scheduling knobs of the GPU path (see spmm_boo_plan_build in spmm_amd.h).
-MAX_ITEM_NNZ = 4096        # a heavier row group is cut into several work items
+# Scheduling knobs of the GPU path (spmm_boo_stage_create in spmm_amd.h).
+MAX_ITEM_NNZ = 4096        # a heavier 32-row slice is cut into several work items
 LONG_ROW_THRESHOLD = 256   # longer remainder rows go to the split-row pass
+WAVES_PER_CU = 16          # persistent waves per compute unit (4 per SIMD at <= 128 VGPRs)
+GROUP = 4                  # slices sharing X tiles per workgroup
 
 
 class BooNzOrder(enum.IntEnum):
@@ -138,8 +140,10 @@ _CLASS = {(np.dtype(c.index_dtype), np.dtype(c.scalar_dtype)): c
 # ---------------------------------------------------------------------------
 
 def _pinned(arr, device, dtype=None):
-    t = torch.from_numpy(np.ascontiguousarray(arr, dtype=dtype))
-    return t.pin_memory().to(device, non_blocking=True)
+    a = np.ascontiguousarray(arr, dtype=dtype)
+    if not a.flags.writeable:
+        a = a.copy()
+    return torch.from_numpy(a).pin_memory().to(device, non_blocking=True)
 
 
 def _rowmajor_copy(blk_nz_ptr, nz_idx, nz_val):
@@ -193,11 +197,25 @@ def _boo_to(self, device='cuda'):
     else:
         k_rem = (d['rem_indptr'], d['rem_col_ind'], d['rem_vals'])
     k_rem_indptr = np.ascontiguousarray(k_rem[0], dtype=i32)
-    plan = core.boo_plan(int(self.rows), self.num_row_groups(),
-                         np.ascontiguousarray(d['row_grp_ptr'], dtype=i32),
-                         np.ascontiguousarray(d['blk_row_grp'], dtype=i32),
-                         np.ascontiguousarray(d['blk_nz_ptr'], dtype=i32),
-                         k_rem_indptr, MAX_ITEM_NNZ, LONG_ROW_THRESHOLD)
+    k_rem_col = np.ascontiguousarray(k_rem[1], dtype=i32)
+    k_rem_val = np.ascontiguousarray(k_rem[2])
+    n_cu = torch.cuda.get_device_properties(device).multi_processor_count
+    host = {
+        'rows': int(self.rows), 'cols': int(self.cols), 'n_row_groups': self.num_row_groups(),
+        'n_col_groups': self.num_col_groups(), 'num_blocks': self.num_blocks(),
+        'row_grp_ptr': np.ascontiguousarray(d['row_grp_ptr'], dtype=i32),
+        'row_ids': np.ascontiguousarray(d['row_ids'], dtype=i32),
+        'col_grp_ptr': np.ascontiguousarray(d['col_grp_ptr'], dtype=i32),
+        'col_ids': np.ascontiguousarray(d['col_ids'], dtype=i32),
+        'blk_row_grp': np.ascontiguousarray(d['blk_row_grp'], dtype=i32),
+        'blk_col_grp': np.ascontiguousarray(d['blk_col_grp'], dtype=i32),
+        'blk_nz_ptr': np.ascontiguousarray(d['blk_nz_ptr'], dtype=i32),
+        'blk_shift': np.ascontiguousarray(d['blk_shift'], dtype=np.uint8),
+        'nz_idx': np.ascontiguousarray(k_idx, dtype=np.uint16),
+        'nz_val': np.ascontiguousarray(k_val),
+        'rem_indptr': k_rem_indptr, 'rem_col_ind': k_rem_col, 'rem_vals': k_rem_val,
+    }
+    stage = core.boo_stage(host, MAX_ITEM_NNZ, LONG_ROW_THRESHOLD, max(GROUP, n_cu * WAVES_PER_CU), GROUP)
 
     # Field names and dtypes of the reference's _gpu_meta (boo.py:72-92) ...
     meta = types.SimpleNamespace(
@@ -218,41 +236,32 @@ def _boo_to(self, device='cuda'):
         tail_col=_pinned(d['tail_col'], device, i32),
         tail_val=_pinned(d['tail_val'], device),
     )
-    # ... plus what the row-group kernel reads: row-major nonzeros, the
-    # remainder with the tail folded in, and the work schedule.
-    if k_idx is nz_idx:
-        meta.k_nz_idx, meta.k_nz_val = meta.nz_idx, meta.nz_val
-    else:
-        meta.k_nz_idx = _pinned(np.ascontiguousarray(k_idx).view(np.int16), device)
-        meta.k_nz_val = _pinned(k_val, device)
+    # ... plus the kernel's tile stream (spmm_boo_stage_*) and the remainder
+    # CSR with the tail folded in, read by the long-row pass.
+    meta.stage = types.SimpleNamespace(**{k: _pinned(stage[k], device) for k in (
+        'tiles', 'tile_rs', 'ent_val', 'ent_col', 'tcols', 'splits', 'long_rows',
+        'wave_tiles')})
     if self.tail_nnz():
         meta.k_rem_indptr = _pinned(k_rem_indptr, device)
-        meta.k_rem_col_ind = _pinned(k_rem[1], device, i32)
-        meta.k_rem_vals = _pinned(k_rem[2], device)
+        meta.k_rem_col_ind = _pinned(k_rem_col, device)
+        meta.k_rem_vals = _pinned(k_rem_val, device)
     else:
         meta.k_rem_indptr, meta.k_rem_col_ind, meta.k_rem_vals = (
             meta.rem_indptr, meta.rem_col_ind, meta.rem_vals)
-    meta.items = _pinned(plan['items'], device, i32)
-    meta.splits = _pinned(plan['splits'], device, i32)
-    meta.long_rows = _pinned(plan['long_rows'], device, i32)
     torch.cuda.synchronize(device)
 
     p = lambda t: int(t.data_ptr())  # noqa: E731
+    g = meta.stage
     meta.desc = {
-        'rows': int(self.rows), 'cols': int(self.cols),
-        'n_row_groups': self.num_row_groups(), 'n_col_groups': self.num_col_groups(),
-        'num_blocks': self.num_blocks(), 'max_nr': int(self.max_nr), 'max_nc': int(self.max_nc),
-        'max_nnz_blk': int(self.max_nnz_blk),
-        'row_grp_ptr': p(meta.row_grp_ptr), 'row_ids': p(meta.row_ids),
-        'col_grp_ptr': p(meta.col_grp_ptr), 'col_ids': p(meta.col_ids),
-        'blk_col_grp': p(meta.blk_col_grp), 'blk_nz_ptr': p(meta.blk_nz_ptr),
-        'blk_shift': p(meta.blk_shift), 'nz_idx': p(meta.k_nz_idx), 'nz_val': p(meta.k_nz_val),
+        'rows': int(self.rows), 'cols': int(self.cols), 'row_ids': p(meta.row_ids),
+        'n_tiles': int(stage['n_tiles']), 'tiles': p(g.tiles),
+        'tile_rs': p(g.tile_rs), 'ent_val': p(g.ent_val), 'ent_col': p(g.ent_col),
+        'tcols': p(g.tcols), 'n_waves': int(stage['n_waves']), 'group': int(stage['group']),
+        'wave_tiles': p(g.wave_tiles),
+        'n_slots': int(stage['n_slots']), 'n_splits': int(stage['n_splits']), 'splits': p(g.splits),
+        'n_long': int(stage['n_long']), 'long_rows': p(g.long_rows),
         'rem_indptr': p(meta.k_rem_indptr), 'rem_col_ind': p(meta.k_rem_col_ind),
         'rem_vals': p(meta.k_rem_vals),
-        'n_items': int(plan['n_items']), 'items': p(meta.items),
-        'n_slots': int(plan['n_slots']), 'n_splits': int(plan['n_splits']),
-        'splits': p(meta.splits), 'n_long': int(plan['n_long']), 'long_rows': p(meta.long_rows),
-        'long_threshold': LONG_ROW_THRESHOLD,
     }
     self._gpu_meta = meta
     return self

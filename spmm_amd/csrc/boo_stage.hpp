@@ -1,0 +1,525 @@
+// Host-side staging of a BOO matrix into the tile stream the gfx950 kernel
+// reads (no device work here).
+//
+// csr_to_boo (boo_matrix/boo_matrix.cpp:53-274) emits row groups, column
+// groups, blocks with uint16 local indices sorted row-major inside each block,
+// and a remainder CSR.  The kernel wants fixed-size units it can prefetch
+// several steps ahead without any dependent lookup, so every row group is cut
+// into 32-row slices and each slice's work into tiles:
+//
+//   * a tile is <= 32 rows x <= 32 columns with <= 128 entries, its entries
+//     sorted by local row (the block's row-major order is kept), each entry a
+//     value plus a one-byte local column, and a 33-entry row-start table;
+//   * a block contributes one tile per 32-column chunk of its column group
+//     (a chunk too full for 128 entries is cut between rows);
+//   * the slice's short remainder rows (<= long_threshold entries) contribute
+//     tiles over the sorted set of their distinct columns, 32 at a time;
+//     longer rows are listed for the split-row pass;
+//   * a slice with no entries still gets one empty tile, so its Y rows are
+//     written (zeros);
+//   * a tile whose entries crowd into a few rows (a remainder row, say) is
+//     flagged to be computed one busy row at a time with lanes along K.
+//
+// A slice is one item unless its entries exceed max_item_nnz; then it is cut
+// at tile boundaries into several items: the first stores Y, the others write
+// partial sums to workspace slots that a fixup pass adds in slot order.
+// Items are dealt to n_waves persistent waves as contiguous ranges of roughly
+// equal cost.  Column ids of block tiles point into col_ids; those of
+// remainder tiles are appended after it in the same array.
+#pragma once
+
+#include <algorithm>
+#include <cstdint>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace spmm_stage {
+
+constexpr int TILE_ROWS = 32;
+constexpr int TILE_COLS = 32;
+constexpr int TILE_ENT = 128;
+constexpr int TILE_RS = TILE_ROWS + 1;
+constexpr int TILE_WORDS = 8;
+constexpr uint32_t FLAG_LAST = 1u;    // last tile of its item
+constexpr uint32_t FLAG_SERIAL = 2u;  // computed one busy row at a time
+constexpr int SERIAL_MAX_BUSY = 8;    // busy rows a serial tile may have
+
+// Cost model for dealing groups to workgroups, in units of one entry's work:
+// a step (X tile staged, workgroup synchronised) and finishing an item.
+constexpr long long COST_STEP = 256;
+constexpr long long COST_ITEM = 512;
+
+struct Staged {
+    // [n_tiles][8]: ent_off, nnz|nc<<8|nr<<16|flags<<24, cid_off, row_off, slot, 0, 0, 0
+    // (slot -1: the item stores Y; otherwise its partial slot)
+    std::vector<int32_t> tiles;
+    std::vector<uint16_t> tile_rs;   // [n_tiles][33]: row starts relative to ent_off
+    std::vector<uint8_t> ent_col;    // [n_ent] (zero padding after odd tiles and at the end)
+    std::vector<char> ent_val;       // [n_ent] values (float or double bytes)
+    std::vector<int32_t> tcols;      // [cols + extra]: col_ids, then remainder tile columns
+    std::vector<int32_t> splits;     // [n_splits][4]: row_off, nr, slot_begin, slot_end
+    std::vector<int32_t> long_rows;  // rows whose remainder exceeds long_threshold
+    std::vector<int32_t> wave_tiles; // [n_waves+1]
+    int32_t n_slots = 0;
+    int32_t n_waves = 0;
+    int32_t group = 1;               // waves per workgroup sharing X tiles
+    size_t n_tiles() const { return tiles.size() / TILE_WORDS; }
+};
+
+// One nonzero on its way into a tile.
+struct Ent {
+    int32_t src;      // index of the value in its source array
+    uint8_t lr;       // local row in the slice
+    uint8_t lc;       // local column in the tile
+    uint8_t from_rem; // value comes from rem_vals rather than nz_val
+    uint8_t pad;
+};
+
+template <typename T>
+class Builder {
+public:
+    struct In {
+        int32_t rows, cols, n_row_groups, n_col_groups, num_blocks;
+        const int32_t *row_grp_ptr, *row_ids, *col_grp_ptr, *col_ids;
+        const int32_t *blk_row_grp, *blk_col_grp, *blk_nz_ptr;
+        const uint8_t* blk_shift;
+        const uint16_t* nz_idx;
+        const T* nz_val;
+        const int32_t *rem_indptr, *rem_col_ind;
+        const T* rem_vals;
+    };
+
+    Builder(const In& in, int max_item_nnz, int long_threshold, int n_waves, int group)
+        : in_(in), max_item_nnz_(max_item_nnz), long_threshold_(long_threshold),
+          want_waves_(n_waves), G_(group) {}
+
+    void run(Staged& S) {
+        S = Staged();
+        S.group = G_;
+        S.tcols.assign(in_.col_ids, in_.col_ids + in_.cols);
+        collect_slices(S);
+        make_groups();
+        for (size_t g = 0; g < groups_.size(); ++g) build_group_steps(S, g);
+        deal_and_emit(S);
+    }
+
+private:
+    // ---- a 32-row slice of a row group: its block chunks and short remainder
+    struct Chunk {
+        int cid_off, nc;
+        size_t e0, e1;  // entries in pool_, row-major
+    };
+    struct Slice {
+        int row_off, nr;
+        size_t c0, c1;  // chunks in chunks_
+        size_t r0, r1;  // remainder entries in pool_ (lc = 0; column in rcol_)
+        long long nnz;
+    };
+    // ---- one step of a group: one X tile, each member's entries in it
+    struct Step {
+        int cid_off, nc;
+        size_t m0;      // member pieces in pieces_ [m0, m0 + G)
+    };
+    struct Piece {
+        size_t e0, e1;  // entries in tent_ (lc = tile-local column)
+    };
+    struct Group {
+        int members[4];
+        int n_members;
+        size_t s0, s1;  // steps in steps_
+        long long cost;
+    };
+
+    void collect_slices(Staged& S) {
+        int blk = 0;
+        std::vector<Ent> ents;
+        for (int rg = 0; rg < in_.n_row_groups; ++rg) {
+            const int r0 = in_.row_grp_ptr[rg];
+            const int nr_g = in_.row_grp_ptr[rg + 1] - r0;
+            if (nr_g < 0) throw std::invalid_argument("row_grp_ptr is not nondecreasing");
+            const int bb = blk;
+            while (blk < in_.num_blocks && in_.blk_row_grp[blk] == rg) ++blk;
+            if (blk < in_.num_blocks && in_.blk_row_grp[blk] < rg)
+                throw std::invalid_argument("blocks are not sorted by row group");
+            const int be = blk;
+            for (int s0 = 0; s0 < nr_g; s0 += TILE_ROWS) {
+                Slice sl;
+                sl.nr = std::min(TILE_ROWS, nr_g - s0);
+                sl.row_off = r0 + s0;
+                sl.c0 = chunks_.size();
+                sl.nnz = 0;
+                for (int b = bb; b < be; ++b) {
+                    const int cg = in_.blk_col_grp[b];
+                    if (cg < 0 || cg >= in_.n_col_groups) throw std::invalid_argument("blk_col_grp out of range");
+                    const int c0 = in_.col_grp_ptr[cg];
+                    const int ncb = in_.col_grp_ptr[cg + 1] - c0;
+                    const int sh = in_.blk_shift[b];
+                    const uint32_t mask = (1u << sh) - 1u;
+                    const int e0 = in_.blk_nz_ptr[b], e1 = in_.blk_nz_ptr[b + 1];
+                    ents.clear();
+                    int prev_row = -1;
+                    for (int e = e0; e < e1; ++e) {
+                        const int row = (int)((uint32_t)in_.nz_idx[e] >> sh);
+                        const int col = (int)((uint32_t)in_.nz_idx[e] & mask);
+                        if (row < prev_row) throw std::invalid_argument("block entries are not row-major");
+                        prev_row = row;
+                        if (row >= nr_g || col >= ncb) throw std::invalid_argument("block entry out of range");
+                        if (row < s0 || row >= s0 + sl.nr) continue;
+                        ents.push_back(Ent{e, (uint8_t)(row - s0), 0, 0, 0});
+                        colx_.push_back(col);
+                    }
+                    if (ents.empty()) continue;
+                    // one chunk per 32 columns of the column group
+                    const size_t cx0 = colx_.size() - ents.size();
+                    for (int k0 = 0; k0 < ncb; k0 += TILE_COLS) {
+                        const size_t p0 = pool_.size();
+                        for (size_t u = 0; u < ents.size(); ++u) {
+                            const int col = colx_[cx0 + u];
+                            if (col >= k0 && col < k0 + TILE_COLS) {
+                                Ent x = ents[u];
+                                x.lc = (uint8_t)(col - k0);
+                                pool_.push_back(x);
+                            }
+                        }
+                        if (pool_.size() > p0)
+                            chunks_.push_back(Chunk{c0 + k0, std::min(TILE_COLS, ncb - k0), p0, pool_.size()});
+                    }
+                    colx_.resize(cx0);
+                    sl.nnz += (long long)ents.size();
+                }
+                sl.c1 = chunks_.size();
+                sl.r0 = pool_.size();
+                for (int lr = 0; lr < sl.nr; ++lr) {
+                    const int row = in_.row_ids[sl.row_off + lr];
+                    if (row < 0 || row >= in_.rows) throw std::invalid_argument("row_ids out of range");
+                    const int rs = in_.rem_indptr[row], re = in_.rem_indptr[row + 1];
+                    if (re == rs) continue;
+                    if (re - rs > long_threshold_) {
+                        S.long_rows.push_back(row);
+                        continue;
+                    }
+                    for (int j = rs; j < re; ++j) {
+                        pool_.push_back(Ent{j, (uint8_t)lr, 0, 1, 0});
+                        rcol_.resize(pool_.size());
+                        rcol_.back() = in_.rem_col_ind[j];
+                    }
+                    sl.nnz += re - rs;
+                }
+                sl.r1 = pool_.size();
+                slices_.push_back(sl);
+            }
+        }
+        if (blk != in_.num_blocks) throw std::invalid_argument("block row groups out of range");
+        rcol_.resize(pool_.size());
+    }
+
+    // Slices that share column chunks go into one group (up to G): a group
+    // loads each chunk's X tile once for all its members.  Greedy: take the
+    // first free slice, then repeatedly the free slice with the most chunks in
+    // common with the group so far (ties: lowest index).  A slice heavier than
+    // max_item_nnz stays alone (it is cut into several items).
+    void make_groups() {
+        const int ns = (int)slices_.size();
+        std::vector<std::pair<int, int>> kv;  // (chunk key, slice)
+        kv.reserve(chunks_.size());
+        for (int i = 0; i < ns; ++i)
+            for (size_t c = slices_[i].c0; c < slices_[i].c1; ++c) kv.emplace_back(chunks_[c].cid_off, i);
+        std::sort(kv.begin(), kv.end());
+        auto heavy = [&](int i) { return slices_[i].nnz > max_item_nnz_; };
+        std::vector<char> used(ns, 0);
+        std::vector<int> score(ns, 0), touched;
+        std::vector<int> keys;
+        int fill = 0;
+        for (int i = 0; i < ns; ++i) {
+            if (used[i]) continue;
+            Group g{};
+            g.members[0] = i;
+            g.n_members = 1;
+            used[i] = 1;
+            if (G_ > 1 && !heavy(i)) {
+                keys.clear();
+                touched.clear();
+                auto add_keys = [&](int s) {
+                    for (size_t c = slices_[s].c0; c < slices_[s].c1; ++c) {
+                        const int k = chunks_[c].cid_off;
+                        if (std::find(keys.begin(), keys.end(), k) != keys.end()) continue;
+                        keys.push_back(k);
+                        // candidates: the next few slices (in order) that share the key
+                        auto it = std::lower_bound(kv.begin(), kv.end(), std::make_pair(k, i));
+                        for (int n = 0; it != kv.end() && it->first == k && n < 64; ++it, ++n) {
+                            const int o = it->second;
+                            if (used[o] || heavy(o)) continue;
+                            if (score[o] == 0) touched.push_back(o);
+                            ++score[o];
+                        }
+                    }
+                };
+                add_keys(i);
+                while (g.n_members < G_) {
+                    int best = -1;
+                    for (int o : touched)
+                        if (!used[o] && score[o] > 0 && (best < 0 || score[o] > score[best] ||
+                                                         (score[o] == score[best] && o < best)))
+                            best = o;
+                    if (best < 0) {
+                        // nothing shares a chunk: fill with the next free slice,
+                        // so the number of groups stays near slices / G
+                        while (fill < ns && (used[fill] || heavy(fill))) ++fill;
+                        if (fill >= ns) break;
+                        best = fill;
+                    }
+                    used[best] = 1;
+                    g.members[g.n_members++] = best;
+                    add_keys(best);
+                }
+                for (int o : touched) score[o] = 0;
+            }
+            groups_.push_back(g);
+        }
+    }
+
+    // Cut a member's entries [e0, e1) of tent_ (row-major) between rows into
+    // pieces of at most TILE_ENT entries.
+    static void cut(const std::vector<Ent>& v, size_t e0, size_t e1, std::vector<Piece>& out) {
+        size_t i = e0;
+        do {
+            const size_t start = i;
+            while (i < e1) {
+                size_t j = i;
+                while (j < e1 && v[j].lr == v[i].lr) ++j;
+                if (j - start > (size_t)TILE_ENT && i > start) break;
+                i = j;
+            }
+            out.push_back(Piece{start, i});
+        } while (i < e1);
+    }
+
+    // Append steps for one X tile shared by the members: member m's entries
+    // are tent_[range[m]]; pieces too large are cut into extra steps.
+    void add_steps(int cid_off, int nc, const std::vector<std::pair<size_t, size_t>>& range) {
+        std::vector<std::vector<Piece>> pcs(G_);
+        size_t n = 1;
+        for (int m = 0; m < G_; ++m) {
+            if (range[m].second > range[m].first) cut(tent_, range[m].first, range[m].second, pcs[m]);
+            n = std::max(n, pcs[m].size());
+        }
+        for (size_t k = 0; k < n; ++k) {
+            steps_.push_back(Step{cid_off, nc, pieces_.size()});
+            for (int m = 0; m < G_; ++m)
+                pieces_.push_back(k < pcs[m].size() ? pcs[m][k] : Piece{0, 0});
+        }
+    }
+
+    void build_group_steps(Staged& S, size_t gi) {
+        Group& g = groups_[gi];
+        g.s0 = steps_.size();
+        // block chunks, by key
+        std::vector<std::pair<int, std::pair<int, size_t>>> keyed;  // (key, (member, chunk))
+        for (int m = 0; m < g.n_members; ++m) {
+            const Slice& sl = slices_[g.members[m]];
+            for (size_t c = sl.c0; c < sl.c1; ++c) keyed.push_back({chunks_[c].cid_off, {m, c}});
+        }
+        std::sort(keyed.begin(), keyed.end());
+        std::vector<std::pair<size_t, size_t>> range(G_);
+        for (size_t i = 0; i < keyed.size();) {
+            size_t j = i;
+            for (auto& r : range) r = {0, 0};
+            const Chunk& c0 = chunks_[keyed[i].second.second];
+            while (j < keyed.size() && keyed[j].first == keyed[i].first) {
+                const Chunk& c = chunks_[keyed[j].second.second];
+                const size_t t0 = tent_.size();
+                tent_.insert(tent_.end(), pool_.begin() + c.e0, pool_.begin() + c.e1);
+                range[keyed[j].second.first] = {t0, tent_.size()};
+                ++j;
+            }
+            add_steps(c0.cid_off, c0.nc, range);
+            i = j;
+        }
+        // short remainder rows: tiles over the members' distinct columns
+        std::vector<int32_t> ucols;
+        for (int m = 0; m < g.n_members; ++m) {
+            const Slice& sl = slices_[g.members[m]];
+            for (size_t e = sl.r0; e < sl.r1; ++e) ucols.push_back(rcol_[e]);
+        }
+        if (!ucols.empty()) {
+            std::sort(ucols.begin(), ucols.end());
+            ucols.erase(std::unique(ucols.begin(), ucols.end()), ucols.end());
+            for (size_t k0 = 0; k0 < ucols.size(); k0 += TILE_COLS) {
+                const size_t k1 = std::min(ucols.size(), k0 + TILE_COLS);
+                for (auto& r : range) r = {0, 0};
+                for (int m = 0; m < g.n_members; ++m) {
+                    const Slice& sl = slices_[g.members[m]];
+                    const size_t t0 = tent_.size();
+                    for (size_t e = sl.r0; e < sl.r1; ++e) {
+                        const int col = rcol_[e];
+                        if (col < ucols[k0] || col > ucols[k1 - 1]) continue;
+                        Ent x = pool_[e];
+                        x.lc = (uint8_t)(std::lower_bound(ucols.begin() + k0, ucols.begin() + k1, col) -
+                                         (ucols.begin() + k0));
+                        tent_.push_back(x);
+                    }
+                    range[m] = {t0, tent_.size()};
+                }
+                const int cid_off = (int)S.tcols.size();
+                S.tcols.insert(S.tcols.end(), ucols.begin() + k0, ucols.begin() + k1);
+                add_steps(cid_off, (int)(k1 - k0), range);
+            }
+        }
+        if (steps_.size() == g.s0) {
+            for (auto& r : range) r = {0, 0};
+            add_steps(0, 0, range);
+        }
+        g.s1 = steps_.size();
+        // A step costs about the same whatever its entries (the X tile is
+        // loaded and the workgroup synchronises either way), and entries add
+        // a little on top.
+        long long nnz = 0;
+        for (int m = 0; m < g.n_members; ++m) nnz += slices_[g.members[m]].nnz;
+        g.cost = COST_ITEM + (long long)(g.s1 - g.s0) * COST_STEP + nnz / std::max(g.n_members, 1);
+    }
+
+    // Emit one member's tile of a step.
+    void emit_tile(Staged& S, const Piece& pc, int cid_off, int nc, int row_off, int nr, uint32_t flags,
+                   int slot) {
+        const int nnz = (int)(pc.e1 - pc.e0);
+        const int ent_off = (int)S.ent_col.size();
+        uint16_t rs[TILE_RS];
+        int k = 0;
+        for (int r = 0; r <= TILE_ROWS; ++r) {
+            while (k < nnz && tent_[pc.e0 + k].lr < r) ++k;
+            rs[r] = (uint16_t)k;
+        }
+        for (size_t u = pc.e0; u < pc.e1; ++u) {
+            const Ent& x = tent_[u];
+            S.ent_col.push_back(x.lc);
+            const T v = x.from_rem ? in_.rem_vals[x.src] : in_.nz_val[x.src];
+            const char* p = reinterpret_cast<const char*>(&v);
+            S.ent_val.insert(S.ent_val.end(), p, p + sizeof(T));
+        }
+        // Rows in parallel cost one step per entry of the longest row; one
+        // busy row at a time costs about a tenth of a step per entry plus a
+        // step per busy row to hand its sums over.
+        int busy = 0, longest = 0;
+        for (int r = 0; r < TILE_ROWS; ++r) {
+            const int len = rs[r + 1] - rs[r];
+            busy += len > 0;
+            longest = std::max(longest, len);
+        }
+        if (busy <= SERIAL_MAX_BUSY && 10 * longest > nnz + 10 * busy) flags |= FLAG_SERIAL;
+        const int32_t w[TILE_WORDS] = {ent_off, (int32_t)(nnz | (nc << 8) | (nr << 16) | (flags << 24)),
+                                       cid_off, row_off, slot, 0, 0, 0};
+        S.tiles.insert(S.tiles.end(), w, w + TILE_WORDS);
+        // entries of every tile start at an even index, so the kernel can load
+        // them two at a time
+        if (nnz & 1) {
+            S.ent_col.push_back(0);
+            S.ent_val.insert(S.ent_val.end(), sizeof(T), 0);
+        }
+        S.tile_rs.insert(S.tile_rs.end(), rs, rs + TILE_RS);
+    }
+
+    // Deal groups to workgroups of G waves (contiguous ranges of near-equal
+    // cost), then lay out each wave's stream: for each of its workgroup's
+    // groups, its member's tile of every step.  A slice alone in its group is
+    // cut into items of at most max_item_nnz entries (the first stores Y, the
+    // others partial slots).
+    void deal_and_emit(Staged& S) {
+        const int ng = (int)groups_.size();
+        int nwg = std::max(1, std::min(std::max(want_waves_ / G_, 1), ng));
+        if (ng == 0) {
+            S.wave_tiles.assign(1, 0);
+            S.n_waves = 0;
+            finish(S);
+            return;
+        }
+        // Contiguous ranges (neighbouring groups share X rows in L2) that
+        // minimise the largest range cost: binary search on that bound, each
+        // range filled greedily.
+        long long lo = 0, hi = 0;
+        for (const Group& g : groups_) {
+            lo = std::max(lo, g.cost);
+            hi += g.cost;
+        }
+        auto ranges_for = [&](long long bound, std::vector<int>* first) {
+            int n = 0;
+            long long acc = 0;
+            for (int gi = 0; gi < ng; ++gi) {
+                if (gi == 0 || acc + groups_[gi].cost > bound) {
+                    ++n;
+                    acc = 0;
+                    if (first) first->push_back(gi);
+                }
+                acc += groups_[gi].cost;
+            }
+            return n;
+        };
+        while (lo < hi) {
+            const long long mid = lo + (hi - lo) / 2;
+            if (ranges_for(mid, nullptr) <= nwg) hi = mid;
+            else lo = mid + 1;
+        }
+        std::vector<int> wg_first;
+        ranges_for(lo, &wg_first);
+        nwg = (int)wg_first.size();
+        wg_first.push_back(ng);
+        S.n_waves = nwg * G_;
+        S.wave_tiles.assign(1, 0);
+        for (int w = 0; w < nwg; ++w) {
+            for (int m = 0; m < G_; ++m) {
+                for (int gi = wg_first[w]; gi < wg_first[w + 1]; ++gi) {
+                    const Group& g = groups_[gi];
+                    const bool real = m < g.n_members;
+                    const Slice* sl = real ? &slices_[g.members[m]] : nullptr;
+                    const int row_off = real ? sl->row_off : 0, nr = real ? sl->nr : 0;
+                    // items of this member: cut at max_item_nnz when alone
+                    int slot = -1;
+                    long long nnz = 0;
+                    const int slot_begin = S.n_slots;
+                    for (size_t st = g.s0; st < g.s1; ++st) {
+                        const Step& sp = steps_[st];
+                        const Piece& pc = pieces_[sp.m0 + m];
+                        const long long tn = (long long)(pc.e1 - pc.e0);
+                        uint32_t flags = 0;
+                        if (st + 1 == g.s1) flags |= FLAG_LAST;
+                        if (real && g.n_members == 1 && st + 1 < g.s1) {
+                            const Piece& nx = pieces_[steps_[st + 1].m0 + m];
+                            if (nnz + tn + (long long)(nx.e1 - nx.e0) > max_item_nnz_ && nnz + tn > 0) flags |= FLAG_LAST;
+                        }
+                        emit_tile(S, real ? pc : Piece{0, 0}, sp.cid_off, sp.nc, row_off, nr, flags, slot);
+                        nnz += tn;
+                        if ((flags & FLAG_LAST) && st + 1 < g.s1) {  // next item of a split slice
+                            slot = S.n_slots++;
+                            nnz = 0;
+                        }
+                    }
+                    if (S.n_slots > slot_begin) {
+                        const int32_t sp4[4] = {row_off, nr, slot_begin, S.n_slots};
+                        S.splits.insert(S.splits.end(), sp4, sp4 + 4);
+                    }
+                }
+                S.wave_tiles.push_back((int32_t)S.n_tiles());
+            }
+        }
+        finish(S);
+    }
+
+    void finish(Staged& S) {
+        // Two spare entries past the end: an empty tile's loads are clamped onto them.
+        S.ent_col.insert(S.ent_col.end(), 2, 0);
+        S.ent_val.insert(S.ent_val.end(), 2 * sizeof(T), 0);
+    }
+
+    In in_;
+    int max_item_nnz_, long_threshold_, want_waves_, G_;
+    std::vector<Ent> pool_, tent_;
+    std::vector<int32_t> rcol_, colx_;
+    std::vector<Chunk> chunks_;
+    std::vector<Slice> slices_;
+    std::vector<Group> groups_;
+    std::vector<Step> steps_;
+    std::vector<Piece> pieces_;
+};
+
+}  // namespace spmm_stage

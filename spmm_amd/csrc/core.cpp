@@ -271,60 +271,86 @@ spmm_boo_desc boo_desc(const py::dict& d) {
     spmm_boo_desc A{};
     A.rows = d["rows"].cast<int32_t>();
     A.cols = d["cols"].cast<int32_t>();
-    A.n_row_groups = d["n_row_groups"].cast<int32_t>();
-    A.n_col_groups = d["n_col_groups"].cast<int32_t>();
-    A.num_blocks = d["num_blocks"].cast<int32_t>();
-    A.max_nr = d["max_nr"].cast<int32_t>();
-    A.max_nc = d["max_nc"].cast<int32_t>();
-    A.max_nnz_blk = d["max_nnz_blk"].cast<int32_t>();
-    A.row_grp_ptr = reinterpret_cast<const int32_t*>(P(d, "row_grp_ptr"));
     A.row_ids = reinterpret_cast<const int32_t*>(P(d, "row_ids"));
-    A.col_grp_ptr = reinterpret_cast<const int32_t*>(P(d, "col_grp_ptr"));
-    A.col_ids = reinterpret_cast<const int32_t*>(P(d, "col_ids"));
-    A.blk_col_grp = reinterpret_cast<const int32_t*>(P(d, "blk_col_grp"));
-    A.blk_nz_ptr = reinterpret_cast<const int32_t*>(P(d, "blk_nz_ptr"));
-    A.blk_shift = reinterpret_cast<const uint8_t*>(P(d, "blk_shift"));
-    A.nz_idx = reinterpret_cast<const uint16_t*>(P(d, "nz_idx"));
-    A.nz_val = reinterpret_cast<const void*>(P(d, "nz_val"));
-    A.rem_indptr = reinterpret_cast<const int32_t*>(P(d, "rem_indptr"));
-    A.rem_col_ind = reinterpret_cast<const int32_t*>(P(d, "rem_col_ind"));
-    A.rem_vals = reinterpret_cast<const void*>(P(d, "rem_vals"));
-    A.n_items = d["n_items"].cast<int32_t>();
-    A.items = reinterpret_cast<const int32_t*>(P(d, "items"));
+    A.n_tiles = d["n_tiles"].cast<int32_t>();
+    A.tiles = reinterpret_cast<const int32_t*>(P(d, "tiles"));
+    A.tile_rs = reinterpret_cast<const uint16_t*>(P(d, "tile_rs"));
+    A.ent_val = reinterpret_cast<const void*>(P(d, "ent_val"));
+    A.ent_col = reinterpret_cast<const uint8_t*>(P(d, "ent_col"));
+    A.tcols = reinterpret_cast<const int32_t*>(P(d, "tcols"));
+    A.n_waves = d["n_waves"].cast<int32_t>();
+    A.group = d["group"].cast<int32_t>();
+    A.wave_tiles = reinterpret_cast<const int32_t*>(P(d, "wave_tiles"));
     A.n_slots = d["n_slots"].cast<int32_t>();
     A.n_splits = d["n_splits"].cast<int32_t>();
     A.splits = reinterpret_cast<const int32_t*>(P(d, "splits"));
     A.n_long = d["n_long"].cast<int32_t>();
     A.long_rows = reinterpret_cast<const int32_t*>(P(d, "long_rows"));
-    A.long_threshold = d["long_threshold"].cast<int32_t>();
+    A.rem_indptr = reinterpret_cast<const int32_t*>(P(d, "rem_indptr"));
+    A.rem_col_ind = reinterpret_cast<const int32_t*>(P(d, "rem_col_ind"));
+    A.rem_vals = reinterpret_cast<const void*>(P(d, "rem_vals"));
     return A;
 }
 
-py::dict boo_plan(int32_t rows, int32_t n_rg, const py::array& row_grp_ptr, const py::array& blk_row_grp,
-                  const py::array& blk_nz_ptr, const py::array& rem_indptr, int32_t max_item_nnz,
-                  int32_t long_threshold) {
-    const int32_t* rgp = ptr_of<int32_t>(row_grp_ptr, "row_grp_ptr");
-    const int32_t* brg = ptr_of<int32_t>(blk_row_grp, "blk_row_grp");
-    const int32_t* bnp = ptr_of<int32_t>(blk_nz_ptr, "blk_nz_ptr");
-    const int32_t* rip = ptr_of<int32_t>(rem_indptr, "rem_indptr");
-    const int32_t nb = (int32_t)blk_row_grp.size();
-    int32_t n_items = 0, n_slots = 0, n_splits = 0, n_long = 0;
-    raise_status(spmm_boo_plan_build(rows, n_rg, nb, rgp, brg, bnp, rip, max_item_nnz, long_threshold,
-                                     nullptr, nullptr, 0, nullptr, &n_items, &n_slots, &n_splits, &n_long));
-    std::vector<int32_t> items((size_t)n_items * 4), splits((size_t)n_items * 3), longr((size_t)rows);
-    raise_status(spmm_boo_plan_build(rows, n_rg, nb, rgp, brg, bnp, rip, max_item_nnz, long_threshold,
-                                     items.data(), splits.data(), n_items, longr.data(), &n_items,
-                                     &n_slots, &n_splits, &n_long));
-    splits.resize((size_t)n_splits * 3);
-    longr.resize((size_t)n_long);
+// Host staging of a BOO matrix into the kernel's tile stream (spmm_boo_stage_*).
+// h: the BOO arrays as int32 / uint8 / uint16 numpy arrays plus the sizes.
+py::dict boo_stage(const py::dict& h, int32_t max_item_nnz, int32_t long_threshold, int32_t n_waves,
+                   int32_t group) {
+    auto arr = [&](const char* k) { return h[k].cast<py::array>(); };
+    const py::array nz_val = arr("nz_val"), rem_vals = arr("rem_vals");
+    const bool f64 = is_f64(nz_val);
+    if (f64 != is_f64(rem_vals)) throw std::invalid_argument("nz_val and rem_vals dtypes differ");
+    spmm_boo_host H{};
+    H.rows = h["rows"].cast<int32_t>();
+    H.cols = h["cols"].cast<int32_t>();
+    H.n_row_groups = h["n_row_groups"].cast<int32_t>();
+    H.n_col_groups = h["n_col_groups"].cast<int32_t>();
+    H.num_blocks = h["num_blocks"].cast<int32_t>();
+    H.dtype = f64 ? SPMM_F64 : SPMM_F32;
+    H.row_grp_ptr = ptr_of<int32_t>(arr("row_grp_ptr"), "row_grp_ptr");
+    H.row_ids = ptr_of<int32_t>(arr("row_ids"), "row_ids");
+    H.col_grp_ptr = ptr_of<int32_t>(arr("col_grp_ptr"), "col_grp_ptr");
+    H.col_ids = ptr_of<int32_t>(arr("col_ids"), "col_ids");
+    H.blk_row_grp = ptr_of<int32_t>(arr("blk_row_grp"), "blk_row_grp");
+    H.blk_col_grp = ptr_of<int32_t>(arr("blk_col_grp"), "blk_col_grp");
+    H.blk_nz_ptr = ptr_of<int32_t>(arr("blk_nz_ptr"), "blk_nz_ptr");
+    H.blk_shift = ptr_of<uint8_t>(arr("blk_shift"), "blk_shift");
+    H.nz_idx = ptr_of<uint16_t>(arr("nz_idx"), "nz_idx");
+    H.nz_val = nz_val.data();
+    H.rem_indptr = ptr_of<int32_t>(arr("rem_indptr"), "rem_indptr");
+    H.rem_col_ind = ptr_of<int32_t>(arr("rem_col_ind"), "rem_col_ind");
+    H.rem_vals = rem_vals.data();
+    if (!(nz_val.flags() & py::array::c_style) || !(rem_vals.flags() & py::array::c_style))
+        throw std::invalid_argument("values must be contiguous");
+    spmm_boo_stage* st = nullptr;
+    raise_status(spmm_boo_stage_create(&H, max_item_nnz, long_threshold, n_waves, group, &st));
+    spmm_boo_stage_info inf{};
+    spmm_boo_stage_sizes(st, &inf);
+    std::vector<int32_t> tiles((size_t)inf.n_tiles * 8), tcols((size_t)inf.n_tcols),
+        splits((size_t)inf.n_splits * 4), longr((size_t)inf.n_long), wt((size_t)inf.n_waves + 1);
+    std::vector<uint16_t> rs((size_t)inf.n_tiles * 33);
+    std::vector<uint8_t> ecol((size_t)inf.n_ent);
+    py::array ev = f64 ? py::array(py::array_t<double>((py::ssize_t)inf.n_ent))
+                       : py::array(py::array_t<float>((py::ssize_t)inf.n_ent));
+    const int rc = spmm_boo_stage_copy(st, tiles.data(), rs.data(), inf.n_ent ? ev.mutable_data() : nullptr,
+                                       ecol.data(), tcols.data(), splits.data(), longr.data(), wt.data());
+    spmm_boo_stage_destroy(st);
+    raise_status(rc);
     py::dict d;
-    d["items"] = give(std::move(items));
+    d["tiles"] = give(std::move(tiles));
+    d["tile_rs"] = give(std::move(rs));
+    d["ent_val"] = ev;
+    d["ent_col"] = give(std::move(ecol));
+    d["tcols"] = give(std::move(tcols));
     d["splits"] = give(std::move(splits));
     d["long_rows"] = give(std::move(longr));
-    d["n_items"] = n_items;
-    d["n_slots"] = n_slots;
-    d["n_splits"] = n_splits;
-    d["n_long"] = n_long;
+    d["wave_tiles"] = give(std::move(wt));
+    d["n_tiles"] = inf.n_tiles;
+    d["n_slots"] = inf.n_slots;
+    d["n_splits"] = inf.n_splits;
+    d["n_long"] = inf.n_long;
+    d["n_waves"] = inf.n_waves;
+    d["group"] = inf.group;
     return d;
 }
 
@@ -392,7 +418,8 @@ PYBIND11_MODULE(_core, m) {
         SPMM_DISPATCH_IS(is_i64(d["block_offsets"].cast<py::array>()), is_f64(x), pbr_matmul_cpu_t, d, x, y,
                          batch, K);
     });
-    m.def("boo_plan", &boo_plan);
+    m.def("boo_stage", &boo_stage, py::arg("h"), py::arg("max_item_nnz"), py::arg("long_threshold"),
+          py::arg("n_waves"), py::arg("group") = 1);
     m.def("boo_workspace_bytes", &boo_workspace_bytes);
     m.def("boo_matmul_gpu", &boo_matmul_gpu);
     m.def("pbr_matmul_gpu", &pbr_matmul_gpu);

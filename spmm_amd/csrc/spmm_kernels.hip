@@ -5,16 +5,18 @@
 // per sparse block and merge rows with global atomics into a memset Y --
 // kernels/boo_kernel.cu:410-595, kernels/pbr_kernel.cu:159-326):
 //
-//  * boo_items_kernel -- one wave64 owns one row group (a work item) for one
-//    feature tile.  Lane (r, h) accumulates local row r for half h of the tile
-//    in registers across all of the row group's blocks, then adds the row's
-//    CSR remainder and stores Y once.  For each block the wave builds the
-//    block's row-start table in LDS from nz_idx (sorted row-major, so row r is
-//    the run of entries whose idx >> shift == r) and, when the block reuses
-//    its columns enough, stages the block's gathered X column tile in LDS with
-//    16-byte loads along K.  The LDS row stride is padded by 32 bytes so the
-//    lanes of a wave, which read neighbouring columns, hit distinct banks.
-//  * boo_fixup_kernel -- for row groups too heavy for one item, adds the
+//  * boo_stream_kernel -- persistent waves.  The matrix is staged on the host
+//    into a stream of tiles (<= 32 rows x 32 columns, <= 128 entries, row
+//    starts precomputed; see boo_stage.hpp) and each wave walks a contiguous
+//    range of whole items.  Lane (r, h) accumulates row r for half h of a
+//    64-feature tile in registers across the item's tiles (the BOO blocks,
+//    then the short remainder rows) and stores Y once.  Each tile's X column
+//    tile, entries and row range are loaded D tiles ahead into registers, and
+//    the column ids those loads need D tiles before that, so a step never
+//    waits on a load issued fewer than D steps earlier; the tile is then
+//    written to LDS (row stride padded by 32 bytes so neighbouring columns
+//    fall in distinct banks) and read back by the rows that use it.
+//  * boo_fixup_kernel -- for row slices too heavy for one item, adds the
 //    partial sums of the extra items into Y in slot order (deterministic).
 //  * rows_long_kernel -- remainder rows longer than the long-row threshold:
 //    one workgroup per row, 16 nonzero slots x 16 feature lanes, reduced in a
@@ -36,10 +38,12 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <new>
 #include <string>
 #include <vector>
 
 #include "spmm_amd.h"
+#include "boo_stage.hpp"
 
 namespace {
 
@@ -110,28 +114,27 @@ __device__ __forceinline__ int xcd_remap(int bid, int grid) {
 inline int round_up8(long long n) { return (int)((n + 7) / 8 * 8); }
 
 // ---------------------------------------------------------------------------
-// BOO: row-group items
+// BOO: persistent tile stream
 // ---------------------------------------------------------------------------
 
-constexpr int BOO_TILE_COLS = 32;   // widest column group staged in LDS
-constexpr int BOO_ROWS_PER_WAVE = 32;
+constexpr int ST_ROWS = 32;   // rows of a tile / an item slice (2 lanes per row)
+constexpr int ST_COLS = 32;   // columns (X rows) of a tile
+constexpr int ST_ENT = 128;   // entries of a tile
+constexpr int ST_RS = 33;     // row-start table length
+constexpr int ST_WORDS = 8;   // metadata words per tile
+constexpr int ST_FLAG_LAST = 1;     // last tile of its item: store the rows
+constexpr int ST_FLAG_SERIAL = 2;   // few busy rows: walk them one at a time, lanes along K
 
 template <typename T>
-struct BooArgs {
-    int rows, cols, K, batch, n_items, max_nr, long_threshold;
-    const int* row_grp_ptr;
+struct StreamArgs {
+    int rows, cols, K, batch, n_waves, n_tiles, group;
+    const int* tiles;           // 8 words: ent_off, nnz | nc<<8 | nr<<16 | flags<<24, cid_off, row_off, slot
+    const uint16_t* tile_rs;
+    const T* ent_val;
+    const uint8_t* ent_col;
+    const int* tcols;
     const int* row_ids;
-    const int* col_grp_ptr;
-    const int* col_ids;
-    const int* blk_col_grp;
-    const int* blk_nz_ptr;
-    const uint8_t* blk_shift;
-    const uint16_t* nz_idx;
-    const T* nz_val;
-    const int* rem_indptr;
-    const int* rem_col_ind;
-    const T* rem_vals;
-    const int* items;
+    const int* wave_tiles;
     const T* X;
     T* Y;
     T* P;
@@ -150,15 +153,16 @@ __device__ __forceinline__ const T* xaddr(const T* Xb, int row, int K, int f) {
     }
 }
 
-// LDS copy of one block nonzero: local index and value read by one ds_read.
+// LDS copy of one tile entry: local column and value read by one ds_read.
 template <typename T> struct alignas(2 * sizeof(T) > 8 ? 16 : 8) NzEntry {
-    uint32_t idx;
+    uint32_t col;
     T val;
 };
 
 // Feature tile geometry: lane half h owns the VEC-element chunks 2q+h of the
 // tile, q < NQ.  Interleaving the halves keeps the two lanes of a row on
-// different LDS banks.
+// different LDS banks.  The LDS row stride is padded by 32 bytes so the lanes
+// of a wave, which read neighbouring columns, hit distinct banks.
 template <typename T, int F, int VEC>
 struct BooGeom {
     static constexpr int KT = 2 * F;              // features per tile
@@ -166,37 +170,136 @@ struct BooGeom {
     static constexpr int NQ = F / VEC;            // chunks per lane
     static constexpr int STRIDE = KT + 32 / (int)sizeof(T);  // LDS row stride (elements)
     static constexpr int CPI = 64 / CHUNKS;       // columns staged per wave instruction
+    static constexpr int NST = ST_COLS / CPI;     // staging instructions per tile
     static_assert(CHUNKS <= 64 && 64 % CHUNKS == 0, "tile too wide for one wave");
 };
 
-// Accumulate nonzeros [j, e) of one block for this lane's row into acc.
-// FAST: nonzeros from the LDS copy (nzp, block-relative) and X rows from
-// the LDS tile, so the loop waits only on LDS; otherwise both come from global
-// memory.  The two are separate loops, run by separate block passes, so a
-// fast loop never waits on the vector-memory counter (and so never on the
-// next block's prefetch).
-template <typename T, int F, int VEC, bool FULL, bool A32, bool FAST>
-__device__ __forceinline__ void boo_row_block(
-    T (&acc)[F / VEC][VEC], int j, int e, int nz0, uint32_t mask,
-    const uint16_t* __restrict__ nz_idx, const T* __restrict__ nz_val,
-    const NzEntry<T>* __restrict__ nzp,
-    const int* __restrict__ col_ids, int c0, const T* __restrict__ tile,
-    const T* __restrict__ Xb, int K, int fbase, int h) {
+// Prefetch state of one tile, in two parts with different lead times.
+// Far part: the tile's small streaming arrays (entries, row range, row id,
+// slot), the column ids, and one word of the metadata of a later tile --
+// loaded DF steps ahead, since they come straight from HBM.  Near part: the
+// tile's X column tile, gathered from rows that neighbouring tiles share and
+// so mostly served by L2 -- loaded D steps ahead, once the column ids are in.
+template <typename T> struct Pair;
+template <> struct Pair<float> { typedef float type __attribute__((ext_vector_type(2))); };
+template <> struct Pair<double> { typedef double type __attribute__((ext_vector_type(2))); };
+
+template <typename T>
+struct StFar {
+    typename Pair<T>::type v;  // entries 2*lane, 2*lane+1
+    uint32_t c;                // their local columns (low byte, next byte)
+    int rs0;                   // first entry of this lane's row (the row's end comes from lane+2)
+    int row;                   // this lane's row id
+    int cid;                   // lane & 31: column id (lane & 31) of the tile D steps later (clamped to its last)
+    int meta;                  // lanes 0-7: metadata word (lane) of the tile DF+D steps later
+    int4 m;                    // this tile's metadata words 0-3 (uniform)
+    int slot;                  // its word 4: the item's partial slot, -1 for the owner (uniform)
+};
+
+template <typename T, int F, int VEC, int NW>
+struct StNear {
+    T x[NW][VEC];  // this wave's X instructions: instruction i holds column g*NST + i0 + i, g = lane / CHUNKS
+};
+
+// Orders this wave's LDS writes before its later LDS reads by other lanes.
+// The LDS executes one wave's instructions in order; this only stops the
+// compiler from moving memory operations across the point.
+__device__ __forceinline__ void wave_lds_fence() {
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ int opaque_copy(int v) {
+    int r;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
+
+
+struct TileMeta {
+    int4 m;     // ent_off, nnz | nc<<8 | nr<<16 | flags<<24, cid_off, row_off
+    int slot;
+};
+
+// The metadata of the tile whose 8 words lanes 8k..8k+7 hold in v.
+__device__ __forceinline__ TileMeta meta_of(int v, int k = 0) {
+    TileMeta t;
+    t.m = make_int4(__builtin_amdgcn_readlane(v, 8 * k), __builtin_amdgcn_readlane(v, 8 * k + 1),
+                    __builtin_amdgcn_readlane(v, 8 * k + 2), __builtin_amdgcn_readlane(v, 8 * k + 3));
+    t.slot = __builtin_amdgcn_readlane(v, 8 * k + 4);
+    return t;
+}
+
+// base[idx] with a 32-bit element index: a scalar base plus a 32-bit vector
+// offset, so the address costs one integer op.
+template <typename V>
+__device__ __forceinline__ V ld32(const V* base, uint32_t idx) {
+    return *reinterpret_cast<const V*>(reinterpret_cast<const char*>(base) + (size_t)(idx * (uint32_t)sizeof(V)));
+}
+
+// Far loads of tile t (metadata tm), the column ids of tile tc (metadata mc)
+// and the metadata words of tile tn: six vector loads, the same six whatever
+// the tiles hold (indices are clamped into valid memory instead of
+// branching), so the compiler can count them.
+template <typename T>
+__device__ __forceinline__ void st_issue_far(StFar<T>& fr, const StreamArgs<T>& a, const TileMeta& tm,
+                                             int t, const TileMeta& mc, int tn) {
+    const int lane = threadIdx.x & 63;
+    fr.m = tm.m;
+    fr.slot = tm.slot;
+    const int nnz = tm.m.y & 0xff, nr = (tm.m.y >> 16) & 0xff;
+    const int nc = (mc.m.y >> 8) & 0xff;
+    const int lr = lane >> 1;
+    // entries 2*lane, 2*lane+1 (tiles start at even entries; past nnz: padding)
+    const uint32_t k = (uint32_t)(tm.m.x + 2 * min(lane, max((nnz - 1) >> 1, 0)));
+    fr.v = *reinterpret_cast<const typename Pair<T>::type*>(
+        reinterpret_cast<const char*>(a.ent_val) + (size_t)(k * (uint32_t)sizeof(T)));
+    fr.c = ld32(reinterpret_cast<const uint16_t*>(a.ent_col), k >> 1);
+    fr.rs0 = ld32(a.tile_rs, (uint32_t)t * ST_RS + (uint32_t)lr);
+    fr.row = ld32(a.row_ids, (uint32_t)(tm.m.w + min(lr, max(nr - 1, 0))));
+    fr.cid = ld32(a.tcols, (uint32_t)(mc.m.z + min(lane & 31, max(nc - 1, 0))));
+    fr.meta = ld32(a.tiles, (uint32_t)ST_WORDS * (uint32_t)tn + (uint32_t)(lane & 7));
+}
+
+// Near loads: this wave's share (NW staging instructions starting at i0) of
+// the X column tile whose column ids are in colbuf (all 32 entries hold valid
+// ids, so no load is predicated).
+template <typename T, int F, int VEC, int NW, bool FULL, bool A32>
+__device__ __forceinline__ void st_issue_near(StNear<T, F, VEC, NW>& nr, const StreamArgs<T>& a,
+                                              const int* colbuf, int i0, const T* __restrict__ Xb,
+                                              int fbase) {
+    typedef BooGeom<T, F, VEC> G;
+    const int lane = threadIdx.x & 63;
+    const int g = lane / G::CHUNKS;
+    const int ch = lane % G::CHUNKS;
+    const int f = FULL ? fbase + ch * VEC : min(fbase + ch * VEC, a.K - VEC);
+    int col[NW];
+#pragma unroll
+    for (int i = 0; i < NW; ++i) col[i] = colbuf[g * G::NST + i0 + i];
+    if constexpr (A32) {
+        const uint32_t rowb = (uint32_t)a.K * (uint32_t)sizeof(T);
+        const uint32_t fb = (uint32_t)f * (uint32_t)sizeof(T);
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+            const uint32_t off = __umul24((uint32_t)col[i], rowb) + fb;
+            load_vec<T, VEC>(reinterpret_cast<const T*>(reinterpret_cast<const char*>(Xb) + (size_t)off), nr.x[i]);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NW; ++i) load_vec<T, VEC>(Xb + (size_t)col[i] * a.K + f, nr.x[i]);
+    }
+}
+
+// Accumulate entries [j, e) of the LDS tile into this lane's row.
+template <typename T, int F, int VEC, bool FULL>
+__device__ __forceinline__ void st_row(T (&acc)[F / VEC][VEC], int j, int e,
+                                       const NzEntry<T>* __restrict__ nzp,
+                                       const T* __restrict__ tile, int K, int fbase, int h) {
     typedef BooGeom<T, F, VEC> G;
 #pragma nounroll
     for (; j < e; ++j) {
-        T v;
-        const T* xr;
-        if constexpr (FAST) {
-            const NzEntry<T> ent = nzp[j];
-            const uint32_t c = ent.idx & mask;
-            v = ent.val;
-            xr = tile + c * G::STRIDE + h * VEC;
-        } else {
-            const uint32_t c = (uint32_t)nz_idx[nz0 + j] & mask;
-            v = nz_val[nz0 + j];
-            xr = xaddr<T, A32>(Xb, col_ids[c0 + c], K, fbase + h * VEC);
-        }
+        const NzEntry<T> ent = nzp[j];
+        const T* xr = tile + ent.col * G::STRIDE + h * VEC;
         T x[G::NQ][VEC];
 #pragma unroll
         for (int q = 0; q < G::NQ; ++q)
@@ -205,359 +308,253 @@ __device__ __forceinline__ void boo_row_block(
         for (int q = 0; q < G::NQ; ++q) {
             if (FULL || fbase + (2 * q + h) * VEC < K) {
 #pragma unroll
-                for (int u = 0; u < VEC; ++u) acc[q][u] += v * x[q][u];
+                for (int u = 0; u < VEC; ++u) acc[q][u] += ent.val * x[q][u];
             }
         }
     }
 }
 
-// One CSR row (the remainder) into acc; entries are fetched four at a time so
-// their X loads are in flight together.
-template <typename T, int F, int VEC, bool FULL, bool A32>
-__device__ __forceinline__ void csr_row_accumulate(
-    T (&acc)[F / VEC][VEC], int rs, int re, const int* __restrict__ col_ind,
-    const T* __restrict__ vals, const T* __restrict__ Xb, int K, int fbase, int h) {
-    typedef BooGeom<T, F, VEC> G;
-#pragma nounroll
-    for (int j = rs; j < re; j += 4) {
-        int col[4];
-        T v[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int jj = min(j + u, re - 1);   // in bounds; surplus entries get v = 0
-            col[u] = col_ind[jj];
-            v[u] = j + u < re ? vals[jj] : T(0);
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const T* xr = xaddr<T, A32>(Xb, col[u], K, fbase + h * VEC);
-#pragma unroll
-            for (int q = 0; q < G::NQ; ++q) {
-                if (FULL || fbase + (2 * q + h) * VEC < K) {
-                    T x[VEC];
-                    load_vec<T, VEC>(xr + 2 * q * VEC, x);
-#pragma unroll
-                    for (int e = 0; e < VEC; ++e) acc[q][e] += v[u] * x[e];
-                }
-            }
-        }
-    }
-}
+constexpr int ST_SYN = 8;   // busy rows a serial tile may have
 
-// Few rows with remainder entries: the whole wave takes them one row at a time,
-// lanes along the tile's features, and hands each row's sum to its lane pair
-// through LDS.  This keeps a wave whose remainder sits in 2 of 32 rows from
-// running 30 idle lane pairs through every entry.
-template <typename T, int F, int VEC, bool FULL, bool A32>
-__device__ __forceinline__ void boo_rem_row_serial(
-    T (&acc)[F / VEC][VEC], uint64_t rows, int rem_s, int rem_e,
-    const int* __restrict__ col_ind, const T* __restrict__ vals, const T* __restrict__ Xb,
-    int K, int fbase, int h, T* scratch) {
+// A tile whose entries sit in a few busy rows: the whole wave takes one busy
+// row at a time with lanes along the tile's features, and leaves the row's
+// sums in LDS as row k of syn with a matching entry {k, 1} (nzp[ST_ENT + k]);
+// the row's lanes get that one entry as their range, so the ordinary row pass
+// over syn adds the sums (multiplying by 1 is exact).  busy: bit 2r set for
+// each busy row r; rs: this lane's row range (lane 2r holds row r's),
+// replaced for the busy rows' lanes.
+template <typename T, int F, int VEC, bool FULL>
+__device__ __forceinline__ void st_serial(uint64_t busy, int& rs0, int& rs1, NzEntry<T>* __restrict__ nzp,
+                                          const T* __restrict__ tile, T* __restrict__ syn, int K,
+                                          int fbase) {
     typedef BooGeom<T, F, VEC> G;
-    const int lane = threadIdx.x;
-    const bool fok = lane < G::KT && fbase + lane < K;
-    while (rows) {
-        const int l2 = __builtin_ctzll(rows);      // lane 2r of row r
-        rows &= rows - 1;
-        const int rs = __builtin_amdgcn_readlane(rem_s, l2);
-        const int re = __builtin_amdgcn_readlane(rem_e, l2);
-        T s0 = T(0), s1 = T(0), s2 = T(0), s3 = T(0);
-        int j = rs;
-        for (; j + 4 <= re; j += 4) {
-            const int c0 = col_ind[j], c1 = col_ind[j + 1], c2 = col_ind[j + 2], c3 = col_ind[j + 3];
-            const T v0 = vals[j], v1 = vals[j + 1], v2 = vals[j + 2], v3 = vals[j + 3];
-            if (fok) {
-                s0 += v0 * *xaddr<T, A32>(Xb, c0, K, fbase + lane);
-                s1 += v1 * *xaddr<T, A32>(Xb, c1, K, fbase + lane);
-                s2 += v2 * *xaddr<T, A32>(Xb, c2, K, fbase + lane);
-                s3 += v3 * *xaddr<T, A32>(Xb, c3, K, fbase + lane);
-            }
+    const int lane = threadIdx.x & 63;
+    const bool fok = lane < G::KT && (FULL || fbase + lane < K);
+    const T* xc = tile + (lane < G::KT ? lane : 0);
+    const int in0 = rs0, in1 = rs1;
+    for (int k = 0; busy; ++k) {
+        const int l2 = __builtin_ctzll(busy);
+        busy &= busy - 1;
+        int j = __builtin_amdgcn_readlane(in0, l2);
+        const int e = __builtin_amdgcn_readlane(in1, l2);
+        T s0 = T(0), s1 = T(0);
+        for (; j + 2 <= e; j += 2) {
+            const NzEntry<T> a0 = nzp[j], a1 = nzp[j + 1];
+            s0 += a0.val * xc[a0.col * G::STRIDE];
+            s1 += a1.val * xc[a1.col * G::STRIDE];
         }
-        for (; j < re; ++j) {
-            const int c0 = col_ind[j];
-            const T v0 = vals[j];
-            if (fok) s0 += v0 * *xaddr<T, A32>(Xb, c0, K, fbase + lane);
+        if (j < e) {
+            const NzEntry<T> a0 = nzp[j];
+            s0 += a0.val * xc[a0.col * G::STRIDE];
         }
-        __syncthreads();
-        if (lane < G::KT) scratch[lane] = (s0 + s1) + (s2 + s3);
-        __syncthreads();
+        if (lane < G::KT) syn[k * G::STRIDE + lane] = fok ? s0 + s1 : T(0);
+        if (lane == 0) nzp[ST_ENT + k] = NzEntry<T>{(uint32_t)k, T(1)};
         if ((lane & ~1) == l2) {
-#pragma unroll
-            for (int q = 0; q < G::NQ; ++q) {
-                if (FULL || fbase + (2 * q + h) * VEC < K) {
-                    T x[VEC];
-                    load_vec<T, VEC>(scratch + (2 * q + h) * VEC, x);
-#pragma unroll
-                    for (int u = 0; u < VEC; ++u) acc[q][u] += x[u];
-                }
-            }
+            rs0 = ST_ENT + k;
+            rs1 = ST_ENT + k + 1;
         }
     }
 }
 
-constexpr int BOO_ROW_SERIAL_MAX = 8;   // remainder rows per wave taken one at a time
-constexpr int BOO_NZ_CAP = 128;         // nonzeros of a block staged in LDS
-constexpr int BOO_MAX_ITEM_BLOCKS = 64;  // blocks per work item (one per lane)
-
-// Register state prefetched for one block while the previous one computes.
-template <typename T, int F, int VEC>
-struct BooStage {
-    static constexpr int NST = BOO_TILE_COLS / BooGeom<T, F, VEC>::CPI;
-    T x[NST][VEC];
-    uint32_t idx[2];
-    T val[2];
+// LDS of one workgroup of WG waves: the shared X tile, double-buffered, and
+// per wave its entries, its serial-row sums and its column ids.
+template <typename T, int F, int VEC, int WG>
+struct StLds {
+    typedef BooGeom<T, F, VEC> G;
+    T tile[2][ST_COLS * G::STRIDE];
+    T syn[WG][ST_SYN * G::STRIDE];
+    NzEntry<T> nzp[WG][ST_ENT + ST_SYN];
+    int colbuf[WG][ST_COLS];
 };
 
-// Loads for one fast block.  X: instruction m brings columns
-// [m*CPI, (m+1)*CPI), their ids read from the LDS copy colbuf, which holds 0
-// past nc, so every instruction reads valid memory (rows past nc are never
-// read back) and none needs a branch.  Nonzeros: entries lane and lane+64,
-// clamped into the block.  Nothing here waits on an earlier global load.
-template <typename T, int F, int VEC, bool FULL, bool A32>
-__device__ __forceinline__ void boo_prefetch(BooStage<T, F, VEC>& st, int nz0, int nnz, int nc,
-                                             const int* colbuf, const BooArgs<T>& a,
-                                             const T* __restrict__ Xb, int fbase) {
+// Every wave of the workgroup has written its share of the X tile.  Only LDS
+// writes need to be complete (lgkmcnt), never the loads still in flight.
+template <int WG>
+__device__ __forceinline__ void group_sync() {
+    if constexpr (WG > 1) {
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    } else {
+        wave_lds_fence();
+    }
+}
+
+// Workgroups of WG waves; wave v of workgroup b streams the tiles
+// [wave_tiles[b*WG+v], wave_tiles[b*WG+v+1]) of its items for one feature
+// tile.  The WG streams of a workgroup have equal lengths and, step by step,
+// the same X tile (column chunk), so each wave loads 1/WG of it and the
+// workgroup shares it in LDS (double-buffered: one barrier per step).  A
+// tile's far loads (entries, row range, row id) are issued DF steps before it
+// is computed, together with the column ids of the tile D steps after it and
+// the metadata of the tile DF+D steps after it; its X loads are issued D
+// steps before it is computed.  So every wait is for loads issued at least D
+// steps earlier, and every step issues the same loads, which lets the
+// compiler count them.  Lane (r, h) keeps F accumulators of row r across the
+// item's tiles and stores them once, at the item's last tile (to Y, or to a
+// partial slot of a split item).  Steps past the end of the stream load its
+// last tile (the data is never used) and store nothing.
+template <typename T, int F, int VEC, int D, int DF, int WG, bool FULL, bool A32>
+__global__ void __launch_bounds__(64 * WG) boo_stream_kernel(StreamArgs<T> a, int kt0) {
     typedef BooGeom<T, F, VEC> G;
-    const int lane = threadIdx.x;
-    const int ch = lane % G::CHUNKS;
-    const int f = fbase + ch * VEC;
-    int gcol[BooStage<T, F, VEC>::NST];
-#pragma unroll
-    for (int m = 0; m < BooStage<T, F, VEC>::NST; ++m) gcol[m] = colbuf[m * G::CPI + lane / G::CHUNKS];
-#pragma unroll
-    for (int m = 0; m < BooStage<T, F, VEC>::NST; ++m)
-        if (FULL || f < a.K) load_vec<T, VEC>(xaddr<T, A32>(Xb, gcol[m], a.K, f), st.x[m]);
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-        const int k = nz0 + min(lane + 64 * c, nnz - 1);
-        st.idx[c] = a.nz_idx[k];
-        st.val[c] = a.nz_val[k];
-    }
-}
-
-// Row-start table of local rows [s0, s0+32] for a block whose first entries
-// are in registers (lane k: idx[0] = entry k, idx[1] = entry k+64; nnz < 128):
-// entry k starts the rows in (row(k-1), row(k)], row(-1) = -1, row(nnz) = +inf.
-__device__ __forceinline__ void boo_rowtab_regs(const uint32_t (&idx)[2], int nnz, uint32_t shift,
-                                                int s0, int* rowtab) {
-    const int lane = threadIdx.x;
-    int rk[2];
-#pragma unroll
-    for (int c = 0; c < 2; ++c) rk[c] = lane + 64 * c < nnz ? (int)(idx[c] >> shift) : 0x7fffffff;
-    const int last0 = __builtin_amdgcn_readlane(rk[0], 63);
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-        const int k = lane + 64 * c;
-        int rp = __shfl_up(rk[c], 1);
-        if (lane == 0) rp = (c == 0) ? -1 : last0;
-        if (k <= nnz) {
-            const int lo = max(rp + 1, s0);
-            const int hi = min(rk[c], s0 + BOO_ROWS_PER_WAVE);
-            for (int r = lo; r <= hi; ++r) rowtab[r - s0] = k;
-        }
-    }
-}
-
-// Same table read straight from global memory (blocks of any size).
-__device__ __forceinline__ void boo_rowtab_global(const uint16_t* __restrict__ nz_idx, int nz0,
-                                                  int nnz, uint32_t shift, int s0, int* rowtab) {
-    for (int k = threadIdx.x; k <= nnz; k += 64) {
-        const int rk = k < nnz ? (int)((uint32_t)nz_idx[nz0 + k] >> shift) : 0x7fffffff;
-        const int rp = k > 0 ? (int)((uint32_t)nz_idx[nz0 + k - 1] >> shift) : -1;
-        const int lo = max(rp + 1, s0);
-        const int hi = min(rk, s0 + BOO_ROWS_PER_WAVE);
-        for (int r = lo; r <= hi; ++r) rowtab[r - s0] = k;
-    }
-}
-
-template <typename T, int F, int VEC, bool FULL, bool A32>
-__device__ __forceinline__ void boo_item_body(const BooArgs<T>& a, int item, int kt, int b,
-                                              T* tile, NzEntry<T>* nzp, int* rowtab,
-                                              int* colbuf) {
-    typedef BooGeom<T, F, VEC> G;
-    const int lane = threadIdx.x;
+    constexpr int NW = G::NST / WG;   // X staging instructions per wave
+    static_assert(G::NST % WG == 0, "X tile does not split over the workgroup");
+    static_assert(DF % D == 0 && DF > D && ST_WORDS * (DF + D) <= 64, "bad prefetch depths");
+    __shared__ __attribute__((aligned(16))) StLds<T, F, VEC, WG> L;
+    const int wv = threadIdx.x >> 6;
+    const int w = xcd_remap(blockIdx.x, gridDim.x) * WG + wv;
+    if (w >= a.n_waves) return;  // uniform per workgroup: n_waves is a multiple of WG
+    const int lane = threadIdx.x & 63;
     const int h = lane & 1;
-    const int lr_in = lane >> 1;
-    const int4 it = reinterpret_cast<const int4*>(a.items)[item];
-    const int rg = it.x, b0 = it.y, nblk = it.z - it.y, slot = it.w;
-    const int r0 = a.row_grp_ptr[rg];
-    const int nr = a.row_grp_ptr[rg + 1] - r0;
+    const int lr = lane >> 1;
     const int K = a.K;
-    const int fbase = kt * G::KT;
+    const int fbase = (kt0 + (int)blockIdx.y) * G::KT;
+    const int b = blockIdx.z;
     const T* Xb = a.X + (size_t)b * a.cols * K;
+    const int t0 = a.wave_tiles[w], t1 = a.wave_tiles[w + 1];
+    const int tl = t1 - 1;
+    auto cl = [tl](int t) { return min(t, tl); };
+    int* colbuf = L.colbuf[wv];
+    NzEntry<T>* nzp = L.nzp[wv];
+    T* syn = L.syn[wv];
+    const int i0 = wv * NW;           // first staging instruction of this wave
 
-    // Block metadata, lane i for block b0+i (an item has at most 64 blocks).
-    int m_nz0 = 0, m_nnz = 0, m_sh = 0, m_c0 = 0, m_nc = 0;
-    if (lane < nblk) {
-        const int blk = b0 + lane;
-        const int cg = a.blk_col_grp[blk];
-        m_nz0 = a.blk_nz_ptr[blk];
-        m_nnz = a.blk_nz_ptr[blk + 1] - m_nz0;
-        m_sh = a.blk_shift[blk];
-        m_c0 = a.col_grp_ptr[cg];
-        m_nc = a.col_grp_ptr[cg + 1] - m_c0;
-    }
-    // Fast blocks: the column group fits the LDS tile, the block reuses its
-    // columns (>= 1.5 entries per column) and its entries fit the LDS copy.
-    const bool m_fast = lane < nblk && m_nc <= BOO_TILE_COLS && 2 * m_nnz >= 3 * m_nc &&
-                        m_nnz < BOO_NZ_CAP;
-    const uint64_t fast_set = __ballot(m_fast);
-    const uint64_t slow_set = __ballot(lane < nblk && !m_fast);
-    auto next_of = [](uint64_t set, int after) -> int {  // first member > after, or 64
-        const uint64_t rest = after >= 63 ? 0ull : (set & (~0ull << (after + 1)));
-        return rest ? __builtin_ctzll(rest) : 64;
-    };
-    auto colids_of = [&](int j) -> int {  // lane c: column id c of block j (0 past nc)
-        if (j >= 64) return 0;
-        const int c0 = __builtin_amdgcn_readlane(m_c0, j), nc = __builtin_amdgcn_readlane(m_nc, j);
-        return lane < nc ? a.col_ids[c0 + lane] : 0;
-    };
-
-    for (int s0 = 0; s0 < nr; s0 += BOO_ROWS_PER_WAVE) {
-        const int lr = s0 + lr_in;
-        const bool active = lr < nr;
-        const int row = a.row_ids[r0 + min(lr, nr - 1)];
-        int rem_s = 0, rem_e = 0;
-        if (slot < 0) {
-            rem_s = a.rem_indptr[row];
-            rem_e = a.rem_indptr[row + 1];
+    StFar<T> fr[DF];
+    StNear<T, F, VEC, NW> nr[D];
+    TileMeta msave[DF];   // msave[(t - t0) % DF]: metadata of tile t+DF+D, kept D steps
+    {
+        // metadata of tiles t0 .. t0+DF+D-1 (lanes 8k..8k+7: tile t0+k)
+        const int mw = ld32(a.tiles, (uint32_t)ST_WORDS * (uint32_t)cl(t0 + (lane >> 3)) + (uint32_t)(lane & 7));
+        // column ids of tiles t0 .. t0+D-1
+        int cid0[D];
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+            const int4 m = meta_of(mw, j).m;
+            cid0[j] = ld32(a.tcols, (uint32_t)(m.z + min(lane & 31, max(((m.y >> 8) & 0xff) - 1, 0))));
         }
-        T acc[G::NQ][VEC];
+        // The far loads of tiles t0 .. t0+DF-1 and the X loads of t0 ..
+        // t0+D-1, issued in the order the DF steps before t0 would have
+        // issued them (X of tile u at step u-D, far of tile u at step u-DF),
+        // so the waits the compiler derives for the loop hold from its first
+        // step on.
 #pragma unroll
-        for (int q = 0; q < G::NQ; ++q)
-#pragma unroll
-            for (int u = 0; u < VEC; ++u) acc[q][u] = T(0);
-
-        // ---- pass 1: fast blocks, software-pipelined one block ahead.  The
-        // block's column ids travel through colbuf (LDS) so the prefetch's
-        // address math waits only on LDS, never on outstanding global loads.
-        BooStage<T, F, VEC> st;
-        int j = next_of(fast_set, -1);
-        int jn = next_of(fast_set, j);
-        int colv = 0;
-        if (j < 64) {
-            colv = colids_of(j);
-            __syncthreads();
-            if (lane < BOO_TILE_COLS) colbuf[lane] = colv;
-            __syncthreads();
-            boo_prefetch<T, F, VEC, FULL, A32>(st, __builtin_amdgcn_readlane(m_nz0, j),
-                                          __builtin_amdgcn_readlane(m_nnz, j),
-                                          __builtin_amdgcn_readlane(m_nc, j), colbuf, a, Xb, fbase);
-            colv = colids_of(jn);
-        }
-        while (j < 64) {
-            const int nnz = __builtin_amdgcn_readlane(m_nnz, j);
-            const uint32_t shift = __builtin_amdgcn_readlane(m_sh, j);
-            const int nc = __builtin_amdgcn_readlane(m_nc, j);
-            const uint32_t mask = (1u << shift) - 1u;
-
-            __syncthreads();  // the previous block's readers of LDS are done
-            {
-                const int ch = lane % G::CHUNKS;
-#pragma unroll
-                for (int m = 0; m < BooStage<T, F, VEC>::NST; ++m) {
-                    if (FULL || fbase + ch * VEC < K)
-                        store_vec<T, VEC>(tile + (m * G::CPI + lane / G::CHUNKS) * G::STRIDE + ch * VEC,
-                                          st.x[m]);
-                }
-#pragma unroll
-                for (int c = 0; c < 2; ++c) {
-                    const int k = lane + 64 * c;
-                    if (k < nnz) nzp[k] = NzEntry<T>{st.idx[c], st.val[c]};
-                }
-                if (lane < BOO_TILE_COLS) colbuf[lane] = colv;  // ids of block jn
+        for (int j = 0; j < DF; ++j) {
+            if (j >= DF - D) {
+                const int u = j - (DF - D);
+                if (lane < ST_COLS) colbuf[lane] = cid0[u];
+                wave_lds_fence();
+                st_issue_near<T, F, VEC, NW, FULL, A32>(nr[u], a, colbuf, i0, Xb, fbase);
+                wave_lds_fence();
             }
-            boo_rowtab_regs(st.idx, nnz, shift, s0, rowtab);
-            __syncthreads();
-            // Issue the next fast block's loads; they land while this one computes.
-            const int jnn = next_of(fast_set, jn);
-            if (jn < 64) {
-                boo_prefetch<T, F, VEC, FULL, A32>(st, __builtin_amdgcn_readlane(m_nz0, jn),
-                                              __builtin_amdgcn_readlane(m_nnz, jn),
-                                              __builtin_amdgcn_readlane(m_nc, jn), colbuf, a, Xb,
-                                              fbase);
-                colv = colids_of(jnn);
-            }
-            if (active)
-                boo_row_block<T, F, VEC, FULL, A32, true>(acc, rowtab[lr_in], rowtab[lr_in + 1], 0, mask,
-                                                     a.nz_idx, a.nz_val, nzp, a.col_ids, 0,
-                                                     tile, Xb, K, fbase, h);
-            j = jn;
-            jn = jnn;
-        }
-
-        // ---- pass 2: the other blocks, straight from global memory
-        for (int js = next_of(slow_set, -1); js < 64; js = next_of(slow_set, js)) {
-            const int nz0 = __builtin_amdgcn_readlane(m_nz0, js);
-            const int nnz = __builtin_amdgcn_readlane(m_nnz, js);
-            const uint32_t shift = __builtin_amdgcn_readlane(m_sh, js);
-            const int c0 = __builtin_amdgcn_readlane(m_c0, js);
-            __syncthreads();
-            boo_rowtab_global(a.nz_idx, nz0, nnz, shift, s0, rowtab);
-            __syncthreads();
-            if (active)
-                boo_row_block<T, F, VEC, FULL, A32, false>(acc, rowtab[lr_in], rowtab[lr_in + 1], nz0,
-                                                      (1u << shift) - 1u, a.nz_idx, a.nz_val, nzp,
-                                                      a.col_ids, c0, tile, Xb, K, fbase, h);
-        }
-
-        // ---- remainder rows (short ones; longer rows go to the split-row pass)
-        const bool has_rem = active && slot < 0 && rem_e > rem_s && rem_e - rem_s <= a.long_threshold;
-        const uint64_t rem_rows = __ballot(has_rem && h == 0);
-        if (__popcll(rem_rows) > BOO_ROW_SERIAL_MAX) {
-            // many rows have entries: every lane pair walks its own row
-            if (has_rem)
-                csr_row_accumulate<T, F, VEC, FULL, A32>(acc, rem_s, rem_e, a.rem_col_ind, a.rem_vals,
-                                                    Xb, K, fbase, h);
-        } else if (rem_rows) {
-            boo_rem_row_serial<T, F, VEC, FULL, A32>(acc, rem_rows, rem_s, rem_e, a.rem_col_ind,
-                                                a.rem_vals, Xb, K, fbase, h, tile);
-        }
-        if (!active) continue;
-        T* out;
-        if (slot < 0) {
-            out = a.Y + ((size_t)b * a.rows + row) * K + fbase + h * VEC;
-        } else {
-            out = a.P + (((size_t)slot * a.batch + b) * a.max_nr + lr) * K + fbase + h * VEC;
+            st_issue_far<T>(fr[j], a, meta_of(mw, j), cl(t0 + j), meta_of(mw, j + D), cl(t0 + j + DF + D));
         }
 #pragma unroll
-        for (int q = 0; q < G::NQ; ++q) {
-            if (FULL || fbase + (2 * q + h) * VEC < K) store_vec<T, VEC>(out + 2 * q * VEC, acc[q]);
-        }
+        for (int j = 0; j < D; ++j) msave[(DF - D + j) % DF] = meta_of(mw, DF + j);
     }
-}
 
-template <typename T, int F, int VEC, bool FULL, bool A32>
-__global__ void __launch_bounds__(64) boo_items_kernel(BooArgs<T> a, int kt0) {
-    typedef BooGeom<T, F, VEC> G;
-    __shared__ __attribute__((aligned(16))) T tile[BOO_TILE_COLS * G::STRIDE];
-    __shared__ NzEntry<T> nzp[BOO_NZ_CAP];
-    __shared__ int rowtab[BOO_ROWS_PER_WAVE + 1];
-    __shared__ int colbuf[BOO_TILE_COLS];
-    const int item = xcd_remap(blockIdx.x, gridDim.x);
-    if (item >= a.n_items) return;
-    boo_item_body<T, F, VEC, FULL, A32>(a, item, kt0 + (int)blockIdx.y, blockIdx.z, tile, nzp, rowtab,
-                                        colbuf);
+    T acc[G::NQ][VEC];
+#pragma unroll
+    for (int q = 0; q < G::NQ; ++q)
+#pragma unroll
+        for (int u = 0; u < VEC; ++u) acc[q][u] = T(0);
+
+    // One step: tile t (step n of the stream), whose far loads are in FR and
+    // X loads in NR.  MS is msave[s]; MP is msave[(s - D) mod DF], the
+    // metadata of tile t+DF.
+    auto step = [&](StFar<T>& FR, StNear<T, F, VEC, NW>& NR, TileMeta& MS, const TileMeta& MP, int t,
+                    int n, bool real) {
+        const int4 mt = FR.m;
+        const int nnz = mt.y & 0xff;
+        T* tile = L.tile[n & 1];
+        // (1) this wave's share of X tile t to LDS; entries; column ids of
+        // tile t+D to colbuf
+        {
+            const int g = lane / G::CHUNKS, ch = lane % G::CHUNKS;
+#pragma unroll
+            for (int i = 0; i < NW; ++i) {
+                if (FULL || fbase + ch * VEC < K)
+                    store_vec<T, VEC>(tile + (g * G::NST + i0 + i) * G::STRIDE + ch * VEC, NR.x[i]);
+            }
+            if (2 * lane < nnz) {
+                NzEntry<T>* e = nzp + 2 * lane;
+                e[0] = NzEntry<T>{FR.c & 0xffu, FR.v.x};
+                e[1] = NzEntry<T>{(FR.c >> 8) & 0xffu, FR.v.y};
+            }
+            if (lane < ST_COLS) colbuf[lane] = FR.cid;
+        }
+        // Copies of what this step still needs from FR after FR is refilled.
+        // The copies are opaque to the compiler, so the refill can reuse FR's
+        // registers instead of loading into fresh ones that would then be
+        // copied (and waited for) at the loop back-edge.
+        int rs0 = opaque_copy(FR.rs0);
+        int rs1 = __shfl_down(rs0, 2);          // the next row's start
+        if (lr == ST_ROWS - 1) rs1 = nnz;
+        const int row = opaque_copy(FR.row);
+        const int slot = FR.slot;
+        const TileMeta mfar = MP;                  // tile t+DF
+        const TileMeta mnew = meta_of(FR.meta);    // tile t+DF+D
+        MS = mnew;
+        group_sync<WG>();
+        __builtin_amdgcn_sched_barrier(0);
+        // (2) X loads of tile t+D; far loads of tile t+DF
+        st_issue_near<T, F, VEC, NW, FULL, A32>(NR, a, colbuf, i0, Xb, fbase);
+        st_issue_far<T>(FR, a, mfar, cl(t + DF), mnew, cl(t + 2 * DF + D));
+        __builtin_amdgcn_sched_barrier(0);
+        // (3) tile t (a step past the range recomputes the last tile into an
+        // accumulator that is never stored again)
+        const T* src = tile;
+        if ((mt.y >> 24) & ST_FLAG_SERIAL) {
+            const uint64_t busy = __ballot(h == 0 && rs0 != rs1);
+            st_serial<T, F, VEC, FULL>(busy, rs0, rs1, nzp, tile, syn, K, fbase);
+            wave_lds_fence();
+            src = syn;
+        }
+        st_row<T, F, VEC, FULL>(acc, rs0, rs1, nzp, src, K, fbase, h);
+        wave_lds_fence();
+        // (4) end of the item: store its rows
+        if (real && ((mt.y >> 24) & ST_FLAG_LAST)) {
+            const int nrow = (mt.y >> 16) & 0xff;
+            if (lr < nrow) {
+                T* out = slot < 0 ? a.Y + ((size_t)b * a.rows + row) * K + fbase + h * VEC
+                                  : a.P + (((size_t)slot * a.batch + b) * ST_ROWS + lr) * K + fbase + h * VEC;
+#pragma unroll
+                for (int q = 0; q < G::NQ; ++q)
+                    if (FULL || fbase + (2 * q + h) * VEC < K) store_vec<T, VEC>(out + 2 * q * VEC, acc[q]);
+            }
+#pragma unroll
+            for (int q = 0; q < G::NQ; ++q)
+#pragma unroll
+                for (int u = 0; u < VEC; ++u) acc[q][u] = T(0);
+        }
+    };
+
+    for (int tb = t0; tb < t1; tb += DF) {
+#pragma unroll
+        for (int s = 0; s < DF; ++s)
+            step(fr[s], nr[s % D], msave[s], msave[(s + DF - D) % DF], tb + s, tb + s - t0, tb + s < t1);
+    }
 }
 
 template <typename T>
+__global__ void __launch_bounds__(256) fill_zero_kernel(T* __restrict__ Y, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) Y[i] = T(0);
+}
+
+// Split items: Y[row] += partial slots [slot_begin, slot_end) in slot order.
+template <typename T>
 __global__ void __launch_bounds__(256) boo_fixup_kernel(const int* __restrict__ splits,
-                                                        const int* __restrict__ row_grp_ptr,
                                                         const int* __restrict__ row_ids,
                                                         const T* __restrict__ P, T* __restrict__ Y,
-                                                        int rows, int K, int batch, int max_nr) {
+                                                        int rows, int K, int batch) {
     const int s = blockIdx.x;
     const int b = blockIdx.z;
-    const int rg = splits[3 * s], sb = splits[3 * s + 1], se = splits[3 * s + 2];
-    const int r0 = row_grp_ptr[rg];
-    const int nr = row_grp_ptr[rg + 1] - r0;
+    const int row_off = splits[4 * s], nr = splits[4 * s + 1];
+    const int sb = splits[4 * s + 2], se = splits[4 * s + 3];
     const long long total = (long long)nr * K;
     for (long long e = threadIdx.x; e < total; e += blockDim.x) {
         const int lr = (int)(e / K);
         const int f = (int)(e % K);
-        T* y = Y + ((size_t)b * rows + row_ids[r0 + lr]) * K + f;
+        T* y = Y + ((size_t)b * rows + row_ids[row_off + lr]) * K + f;
         T acc = *y;
-        for (int sl = sb; sl < se; ++sl) acc += P[(((size_t)sl * batch + b) * max_nr + lr) * K + f];
+        for (int sl = sb; sl < se; ++sl) acc += P[(((size_t)sl * batch + b) * ST_ROWS + lr) * K + f];
         *y = acc;
     }
 }
@@ -790,38 +787,56 @@ int boo_pick_f(int K) {
     return f;
 }
 
+#ifndef SPMM_BOO_DEPTH
+#define SPMM_BOO_DEPTH 1        // X tiles loaded this many tiles ahead
+#endif
+#ifndef SPMM_BOO_FAR
+#define SPMM_BOO_FAR 2          // streaming tile data loaded this many tiles ahead
+#endif
+
 // Full feature tiles in one launch, a partial last tile (K % 2F != 0) in a
 // second one compiled with the per-chunk feature guards.
 template <typename T, int F, int VEC, bool A32>
-int launch_boo_items_a(const BooArgs<T>& a, hipStream_t s) {
+int launch_boo_stream_a(const StreamArgs<T>& a, hipStream_t s) {
+    constexpr int D = SPMM_BOO_DEPTH, DF = SPMM_BOO_FAR;
+    constexpr int NST = BooGeom<T, F, VEC>::NST;
+    // Workgroups of 4 waves share X tiles when the staging grouped slices by 4
+    // and the tile splits 4 ways; otherwise each wave is its own workgroup
+    // (every stream is complete on its own, so this is only slower).
+    const bool wg4 = a.group == 4 && NST % 4 == 0;
     const int full = a.K / (2 * F);
+    auto go = [&](auto kern, int wg, int ny, int kt) {
+        const dim3 grid(round_up8(a.n_waves / wg), ny, a.batch);
+        hipLaunchKernelGGL(kern, grid, dim3(64 * wg), 0, s, a, kt);
+        return check_launch("boo_stream_kernel");
+    };
     if (full > 0) {
-        const dim3 grid(round_up8(a.n_items), full, a.batch);
-        hipLaunchKernelGGL((boo_items_kernel<T, F, VEC, true, A32>), grid, dim3(64), 0, s, a, 0);
-        if (int rc = check_launch("boo_items_kernel")) return rc;
+        const int rc = wg4 ? go(boo_stream_kernel<T, F, VEC, D, DF, (NST % 4 == 0 ? 4 : 1), true, A32>, 4, full, 0)
+                           : go(boo_stream_kernel<T, F, VEC, D, DF, 1, true, A32>, 1, full, 0);
+        if (rc) return rc;
     }
     if (a.K % (2 * F)) {
-        const dim3 grid(round_up8(a.n_items), 1, a.batch);
-        hipLaunchKernelGGL((boo_items_kernel<T, F, VEC, false, A32>), grid, dim3(64), 0, s, a, full);
-        return check_launch("boo_items_kernel");
+        return wg4 ? go(boo_stream_kernel<T, F, VEC, D, DF, (NST % 4 == 0 ? 4 : 1), false, A32>, 4, 1, full)
+                   : go(boo_stream_kernel<T, F, VEC, D, DF, 1, false, A32>, 1, 1, full);
     }
     return SPMM_OK;
 }
 
 // 32-bit X addressing when one batch's X slab is under 4 GiB.
 template <typename T, int F, int VEC>
-int launch_boo_items(const BooArgs<T>& a, hipStream_t s) {
-    if ((uint64_t)a.cols * (uint64_t)a.K * sizeof(T) < (1ull << 32))
-        return launch_boo_items_a<T, F, VEC, true>(a, s);
-    return launch_boo_items_a<T, F, VEC, false>(a, s);
+int launch_boo_stream(const StreamArgs<T>& a, hipStream_t s) {
+    if ((uint64_t)a.cols * (uint64_t)a.K * sizeof(T) < (1ull << 32) && a.cols < (1 << 24) &&
+        (uint64_t)a.K * sizeof(T) < (1ull << 24))
+        return launch_boo_stream_a<T, F, VEC, true>(a, s);
+    return launch_boo_stream_a<T, F, VEC, false>(a, s);
 }
 
 template <typename T>
-int boo_dispatch(const BooArgs<T>& a, hipStream_t s) {
+int boo_dispatch(const StreamArgs<T>& a, hipStream_t s) {
     const int F = boo_pick_f<T>(a.K);
     const int VEC = pick_vec<T>(a.K, F, a.X, a.Y);
 #define SPMM_BOO_CASE(FF, VV) \
-    if (F == FF && VEC == VV) return launch_boo_items<T, FF, VV>(a, s);
+    if (F == FF && VEC == VV) return launch_boo_stream<T, FF, VV>(a, s);
     if constexpr (sizeof(T) == 4) {
         SPMM_BOO_CASE(32, 4) SPMM_BOO_CASE(32, 2) SPMM_BOO_CASE(32, 1)
         SPMM_BOO_CASE(16, 4) SPMM_BOO_CASE(16, 2) SPMM_BOO_CASE(16, 1)
@@ -866,34 +881,36 @@ int boo_matmul_t(const spmm_boo_desc* A, const void* Xv, void* Yv, int64_t batch
     const T* X = static_cast<const T*>(Xv);
     T* Y = static_cast<T*>(Yv);
     if (A->rows == 0 || K == 0 || batch == 0) return SPMM_OK;
-    if (A->n_items <= 0 || !A->items) return fail(SPMM_EINVAL, "BOO schedule is empty; build it with spmm_boo_plan_build");
+    if (A->n_waves <= 0 || !A->wave_tiles || !A->tiles)
+        return fail(SPMM_EINVAL, "BOO tile stream is empty; stage the matrix with spmm_boo_stage_create");
     if (A->cols > 0 && !X) return fail(SPMM_EINVAL, "X is null");
     if (!Y) return fail(SPMM_EINVAL, "Y is null");
     const size_t need = spmm_boo_workspace_bytes(A, sizeof(T) == 4 ? SPMM_F32 : SPMM_F64, batch, K);
     if (need > ws_bytes || (need && !ws))
         return fail(SPMM_ENOMEM, "BOO workspace too small: need %zu bytes, got %zu", need, ws_bytes);
 
-    BooArgs<T> a;
+    if (A->cols == 0) {  // no entries: Y = 0
+        const size_t n = (size_t)batch * (size_t)A->rows * (size_t)K;
+        hipLaunchKernelGGL((fill_zero_kernel<T>), dim3((unsigned)std::min<size_t>((n + 255) / 256, 65535)),
+                           dim3(256), 0, s, Y, n);
+        return check_launch("fill_zero_kernel");
+    }
+    StreamArgs<T> a;
     a.rows = A->rows;
     a.cols = A->cols;
     a.K = (int)K;
     a.batch = (int)batch;
-    a.n_items = A->n_items;
-    a.max_nr = A->max_nr;
-    a.long_threshold = A->long_threshold;
-    a.row_grp_ptr = A->row_grp_ptr;
+    a.n_waves = A->n_waves;
+    a.n_tiles = A->n_tiles;
+    a.group = A->group;
+    if (a.group < 1 || a.n_waves % a.group) return fail(SPMM_EINVAL, "n_waves is not a multiple of group");
+    a.tiles = A->tiles;
+    a.tile_rs = A->tile_rs;
+    a.ent_val = static_cast<const T*>(A->ent_val);
+    a.ent_col = A->ent_col;
+    a.tcols = A->tcols;
     a.row_ids = A->row_ids;
-    a.col_grp_ptr = A->col_grp_ptr;
-    a.col_ids = A->col_ids;
-    a.blk_col_grp = A->blk_col_grp;
-    a.blk_nz_ptr = A->blk_nz_ptr;
-    a.blk_shift = A->blk_shift;
-    a.nz_idx = A->nz_idx;
-    a.nz_val = static_cast<const T*>(A->nz_val);
-    a.rem_indptr = A->rem_indptr;
-    a.rem_col_ind = A->rem_col_ind;
-    a.rem_vals = static_cast<const T*>(A->rem_vals);
-    a.items = A->items;
+    a.wave_tiles = A->wave_tiles;
     a.X = X;
     a.Y = Y;
     a.P = static_cast<T*>(ws);
@@ -901,8 +918,8 @@ int boo_matmul_t(const spmm_boo_desc* A, const void* Xv, void* Yv, int64_t batch
     if (rc) return rc;
     if (A->n_splits > 0) {
         const dim3 grid(A->n_splits, 1, (unsigned)batch);
-        hipLaunchKernelGGL((boo_fixup_kernel<T>), grid, dim3(256), 0, s, A->splits, A->row_grp_ptr,
-                           A->row_ids, (const T*)ws, Y, A->rows, (int)K, (int)batch, A->max_nr);
+        hipLaunchKernelGGL((boo_fixup_kernel<T>), grid, dim3(256), 0, s, A->splits, A->row_ids,
+                           (const T*)ws, Y, A->rows, (int)K, (int)batch);
         rc = check_launch("boo_fixup_kernel");
         if (rc) return rc;
     }
@@ -996,77 +1013,99 @@ const char* spmm_last_error(void) { return g_last_error.c_str(); }
 
 const char* spmm_version(void) { return "spmm_amd 0.1 gfx950"; }
 
-int spmm_boo_plan_build(int32_t rows, int32_t n_row_groups, int32_t num_blocks,
-                        const int32_t* h_row_grp_ptr, const int32_t* h_blk_row_grp,
-                        const int32_t* h_blk_nz_ptr, const int32_t* h_rem_indptr,
-                        int32_t max_item_nnz, int32_t long_threshold, int32_t* h_items,
-                        int32_t* h_splits, int32_t item_cap, int32_t* h_long_rows,
-                        int32_t* n_items, int32_t* n_slots, int32_t* n_splits, int32_t* n_long) {
-    if (rows < 0 || n_row_groups < 0 || num_blocks < 0) return fail(SPMM_EINVAL, "negative sizes");
-    if (!h_row_grp_ptr || (num_blocks > 0 && (!h_blk_row_grp || !h_blk_nz_ptr)) || !n_items)
-        return fail(SPMM_EINVAL, "null plan input");
+struct spmm_boo_stage {
+    spmm_stage::Staged s;
+    spmm_dtype dtype;
+};
+
+int spmm_boo_stage_create(const spmm_boo_host* H, int32_t max_item_nnz, int32_t long_threshold,
+                          int32_t n_waves, int32_t group, spmm_boo_stage** out) {
+    if (!H || !out) return fail(SPMM_EINVAL, "null staging argument");
+    *out = nullptr;
+    if (H->rows < 0 || H->cols < 0 || H->n_row_groups < 0 || H->n_col_groups < 0 || H->num_blocks < 0)
+        return fail(SPMM_EINVAL, "negative BOO sizes");
+    if (!H->row_grp_ptr || !H->row_ids || !H->col_grp_ptr || (H->cols > 0 && !H->col_ids) ||
+        !H->rem_indptr || (H->num_blocks > 0 && (!H->blk_row_grp || !H->blk_col_grp || !H->blk_nz_ptr ||
+                                                 !H->blk_shift || !H->nz_idx || !H->nz_val)))
+        return fail(SPMM_EINVAL, "null BOO host array");
     if (max_item_nnz < 1) return fail(SPMM_EINVAL, "max_item_nnz must be positive");
-    int items = 0, slots = 0, splits = 0;
-    int blk = 0;
-    for (int rg = 0; rg < n_row_groups; ++rg) {
-        const int bb = blk;
-        while (blk < num_blocks && h_blk_row_grp[blk] == rg) ++blk;
-        if (blk < num_blocks && h_blk_row_grp[blk] < rg)
-            return fail(SPMM_EINVAL, "blocks are not sorted by row group");
-        const int be = blk;
-        // cut [bb, be) into runs of at most max_item_nnz nonzeros (at least one block each)
-        int start = bb;
-        int first = 1;
-        const int slot_begin = slots;
-        do {
-            int end = start;
-            long long acc = 0;
-            while (end < be && end - start < BOO_MAX_ITEM_BLOCKS) {
-                const long long w = (long long)h_blk_nz_ptr[end + 1] - h_blk_nz_ptr[end];
-                if (end > start && acc + w > max_item_nnz) break;
-                acc += w;
-                ++end;
-            }
-            if (h_items) {
-                if (items >= item_cap) return fail(SPMM_EINVAL, "item_cap too small");
-                h_items[4 * items + 0] = rg;
-                h_items[4 * items + 1] = start;
-                h_items[4 * items + 2] = end;
-                h_items[4 * items + 3] = first ? -1 : slots;
-            }
-            if (!first) ++slots;
-            ++items;
-            first = 0;
-            start = end;
-        } while (start < be);
-        if (slots > slot_begin) {
-            if (h_items && h_splits) {
-                h_splits[3 * splits + 0] = rg;
-                h_splits[3 * splits + 1] = slot_begin;
-                h_splits[3 * splits + 2] = slots;
-            }
-            ++splits;
+    if (n_waves < 1) return fail(SPMM_EINVAL, "n_waves must be positive");
+    if (group != 1 && group != 2 && group != 4) return fail(SPMM_EINVAL, "group must be 1, 2 or 4");
+    if (H->dtype != SPMM_F32 && H->dtype != SPMM_F64) return fail(SPMM_EINVAL, "unknown dtype %d", (int)H->dtype);
+    spmm_boo_stage* st = new (std::nothrow) spmm_boo_stage();
+    if (!st) return fail(SPMM_ENOMEM, "out of host memory");
+    st->dtype = H->dtype;
+    try {
+        if (H->dtype == SPMM_F32) {
+            spmm_stage::Builder<float>::In in{H->rows, H->cols, H->n_row_groups, H->n_col_groups, H->num_blocks,
+                                              H->row_grp_ptr, H->row_ids, H->col_grp_ptr, H->col_ids,
+                                              H->blk_row_grp, H->blk_col_grp, H->blk_nz_ptr, H->blk_shift,
+                                              H->nz_idx, static_cast<const float*>(H->nz_val), H->rem_indptr,
+                                              H->rem_col_ind, static_cast<const float*>(H->rem_vals)};
+            spmm_stage::Builder<float>(in, max_item_nnz, long_threshold, n_waves, group).run(st->s);
+        } else {
+            spmm_stage::Builder<double>::In in{H->rows, H->cols, H->n_row_groups, H->n_col_groups, H->num_blocks,
+                                               H->row_grp_ptr, H->row_ids, H->col_grp_ptr, H->col_ids,
+                                               H->blk_row_grp, H->blk_col_grp, H->blk_nz_ptr, H->blk_shift,
+                                               H->nz_idx, static_cast<const double*>(H->nz_val), H->rem_indptr,
+                                               H->rem_col_ind, static_cast<const double*>(H->rem_vals)};
+            spmm_stage::Builder<double>(in, max_item_nnz, long_threshold, n_waves, group).run(st->s);
         }
+    } catch (const std::invalid_argument& e) {
+        delete st;
+        return fail(SPMM_EINVAL, "%s", e.what());
+    } catch (const std::bad_alloc&) {
+        delete st;
+        return fail(SPMM_ENOMEM, "out of host memory");
     }
-    if (blk != num_blocks) return fail(SPMM_EINVAL, "block row groups out of range");
-    *n_items = items;
-    if (n_slots) *n_slots = slots;
-    if (n_splits) *n_splits = splits;
-    if (h_items) {
-        int nl = 0;
-        if (h_rem_indptr && h_long_rows) {
-            for (int r = 0; r < rows; ++r)
-                if (h_rem_indptr[r + 1] - h_rem_indptr[r] > long_threshold) h_long_rows[nl++] = r;
-        }
-        if (n_long) *n_long = nl;
+    if (st->s.ent_col.size() > (size_t)INT32_MAX || st->s.n_tiles() > (size_t)INT32_MAX / 64 ||
+        st->s.tcols.size() > (size_t)INT32_MAX) {
+        delete st;
+        return fail(SPMM_EUNSUPPORTED, "BOO matrix too large for 32-bit tile offsets");
     }
+    *out = st;
     return SPMM_OK;
 }
+
+int spmm_boo_stage_sizes(const spmm_boo_stage* st, spmm_boo_stage_info* info) {
+    if (!st || !info) return fail(SPMM_EINVAL, "null staging argument");
+    info->n_tiles = (int64_t)st->s.n_tiles();
+    info->n_ent = (int64_t)st->s.ent_col.size();
+    info->n_tcols = (int64_t)st->s.tcols.size();
+    info->n_splits = (int64_t)(st->s.splits.size() / 4);
+    info->n_long = (int64_t)st->s.long_rows.size();
+    info->n_slots = st->s.n_slots;
+    info->n_waves = st->s.n_waves;
+    info->group = st->s.group;
+    return SPMM_OK;
+}
+
+int spmm_boo_stage_copy(const spmm_boo_stage* st, int32_t* tiles, uint16_t* tile_rs,
+                        void* ent_val, uint8_t* ent_col, int32_t* tcols, int32_t* splits,
+                        int32_t* long_rows, int32_t* wave_tiles) {
+    if (!st) return fail(SPMM_EINVAL, "null staging handle");
+    const spmm_stage::Staged& s = st->s;
+    auto put = [](void* dst, const void* src, size_t bytes) {
+        if (bytes && dst) std::memcpy(dst, src, bytes);
+        return bytes == 0 || dst != nullptr;
+    };
+    bool ok = put(tiles, s.tiles.data(), s.tiles.size() * 4) &&
+              put(tile_rs, s.tile_rs.data(), s.tile_rs.size() * 2) &&
+              put(ent_val, s.ent_val.data(), s.ent_val.size()) &&
+              put(ent_col, s.ent_col.data(), s.ent_col.size()) &&
+              put(tcols, s.tcols.data(), s.tcols.size() * 4) &&
+              put(splits, s.splits.data(), s.splits.size() * 4) &&
+              put(long_rows, s.long_rows.data(), s.long_rows.size() * 4) &&
+              put(wave_tiles, s.wave_tiles.data(), s.wave_tiles.size() * 4);
+    return ok ? SPMM_OK : fail(SPMM_EINVAL, "null output array for a non-empty staging field");
+}
+
+void spmm_boo_stage_destroy(spmm_boo_stage* st) { delete st; }
 
 size_t spmm_boo_workspace_bytes(const spmm_boo_desc* A, spmm_dtype dtype, int64_t batch, int64_t K) {
     if (!A || A->n_slots <= 0 || batch <= 0 || K <= 0) return 0;
     const size_t es = dtype == SPMM_F64 ? 8 : 4;
-    return (size_t)A->n_slots * (size_t)batch * (size_t)std::max(A->max_nr, 1) * (size_t)K * es;
+    return (size_t)A->n_slots * (size_t)batch * (size_t)ST_ROWS * (size_t)K * es;
 }
 
 int spmm_boo_matmul(const spmm_boo_desc* A, spmm_dtype dtype, const void* X, void* Y,

@@ -1,0 +1,180 @@
+"""Host staging of BOO into the kernel's tile stream (spmm_boo_stage_* in
+include/spmm_amd.h): every nonzero of the matrix lands in exactly one tile (or
+in a long remainder row), tiles respect their size limits, items and waves
+partition the stream.  CPU only."""
+
+import numpy as np
+import pytest
+import scipy.sparse as sp
+
+import spmm_amd as S
+from spmm_amd import _core
+from spmm_amd import boo as SB
+from spmm_amd import matrices as M
+
+
+def _host(boo):
+    d = boo._d
+    i32 = np.int32
+    nz_idx, nz_val = d['nz_idx'], d['nz_val']
+    if boo.nz_order != SB.BooNzOrder.ROWMAJOR:
+        nz_idx, nz_val = SB._rowmajor_copy(d['blk_nz_ptr'], nz_idx, nz_val)
+    if boo.tail_nnz():
+        rem = SB._merge_tail(boo.rows, d['rem_indptr'], d['rem_col_ind'], d['rem_vals'],
+                             d['tail_row'], d['tail_col'], d['tail_val'])
+    else:
+        rem = (d['rem_indptr'], d['rem_col_ind'], d['rem_vals'])
+    c = lambda a, t=i32: np.ascontiguousarray(a, dtype=t)  # noqa: E731
+    return {
+        'rows': int(boo.rows), 'cols': int(boo.cols), 'n_row_groups': boo.num_row_groups(),
+        'n_col_groups': boo.num_col_groups(), 'num_blocks': boo.num_blocks(),
+        'row_grp_ptr': c(d['row_grp_ptr']), 'row_ids': c(d['row_ids']),
+        'col_grp_ptr': c(d['col_grp_ptr']), 'col_ids': c(d['col_ids']),
+        'blk_row_grp': c(d['blk_row_grp']), 'blk_col_grp': c(d['blk_col_grp']),
+        'blk_nz_ptr': c(d['blk_nz_ptr']), 'blk_shift': c(d['blk_shift'], np.uint8),
+        'nz_idx': c(nz_idx, np.uint16), 'nz_val': np.ascontiguousarray(nz_val),
+        'rem_indptr': c(rem[0]), 'rem_col_ind': c(rem[1]), 'rem_vals': np.ascontiguousarray(rem[2]),
+    }
+
+
+def decode(host, st):
+    """COO (row, col, val) of everything the stream and the long rows hold."""
+    tiles = st['tiles'].reshape(-1, 8)
+    rs = st['tile_rs'].reshape(-1, 33)
+    R, C, V = [], [], []
+    for t, (eo, w1, co, ro, _slot, _, _, _) in enumerate(tiles):
+        assert eo % 2 == 0
+        nnz, nc, nr = w1 & 0xff, (w1 >> 8) & 0xff, (w1 >> 16) & 0xff
+        assert 0 <= nnz <= 128 and 0 <= nc <= 32 and 0 <= nr <= 32
+        assert nr > 0 or nnz == 0                      # nr = 0: a padding wave of a workgroup
+        r = rs[t]
+        assert r[0] == 0 and r[-1] == nnz and np.all(np.diff(r.astype(int)) >= 0)
+        assert np.all(r[nr:] == nnz)                   # rows past the slice hold nothing
+        lr = np.repeat(np.arange(32), np.diff(r.astype(int)))
+        lc = st['ent_col'][eo:eo + nnz].astype(int)
+        assert np.all(lc < nc)
+        R.append(host['row_ids'][ro + lr])
+        C.append(st['tcols'][co + lc])
+        V.append(st['ent_val'][eo:eo + nnz])
+    ip, ci, cv = host['rem_indptr'], host['rem_col_ind'], host['rem_vals']
+    for row in st['long_rows']:
+        R.append(np.full(ip[row + 1] - ip[row], row))
+        C.append(ci[ip[row]:ip[row + 1]])
+        V.append(cv[ip[row]:ip[row + 1]])
+    return np.concatenate(R), np.concatenate(C), np.concatenate(V)
+
+
+def check_stream(A, boo, max_item_nnz=4096, long_thr=256, n_waves=64, group=1):
+    host = _host(boo)
+    st = _core.boo_stage(host, max_item_nnz, long_thr, n_waves, group)
+    r, c, v = decode(host, st)
+    # every stored value exactly once (explicit zeros included)
+    got = sp.coo_matrix((np.ones_like(v, dtype=np.int64), (r, c)), shape=A.shape).tocsr()
+    want = sp.csr_matrix((np.ones(A.nnz, np.int64), A.indices, A.indptr), shape=A.shape)
+    assert (got != want).nnz == 0
+    B = sp.coo_matrix((v, (r, c)), shape=A.shape).tocsr()
+    assert np.array_equal(B.toarray(), A.toarray())
+    # items / waves
+    tiles = st['tiles'].reshape(-1, 8)
+    last = (tiles[:, 1] >> 24) & 1
+    assert last[-1] == 1
+    wt = st['wave_tiles']
+    assert wt[0] == 0 and wt[-1] == len(tiles) and np.all(np.diff(wt) > 0)
+    assert st['n_waves'] == len(wt) - 1 <= max(n_waves, group) and st['n_waves'] % group == 0
+    for w in range(1, len(wt) - 1):
+        assert last[wt[w] - 1] == 1                    # waves hold whole items
+    # the waves of a workgroup walk equal-length streams over the same X tiles
+    lens = np.diff(wt).reshape(-1, group)
+    assert np.all(lens == lens[:, :1])
+    for g0 in range(0, len(wt) - 1, group):
+        base = tiles[wt[g0]:wt[g0 + 1]]
+        for v in range(1, group):
+            other = tiles[wt[g0 + v]:wt[g0 + v + 1]]
+            assert np.array_equal(other[:, 2], base[:, 2])                       # same column chunk
+            assert np.array_equal((other[:, 1] >> 8) & 0xff, (base[:, 1] >> 8) & 0xff)
+    slots = tiles[:, 4]
+    assert np.all(slots[last == 1] >= -1)
+    sl = st['splits'].reshape(-1, 4)
+    assert st['n_slots'] == (sl[:, 3] - sl[:, 2]).sum() if len(sl) else st['n_slots'] == 0
+    long_rows = st['long_rows']
+    lens = np.diff(host['rem_indptr'])
+    assert set(long_rows.tolist()) == set(np.nonzero(lens > long_thr)[0].tolist())
+    return st
+
+
+@pytest.mark.parametrize('policy', ['keep', 'remainder', 'tail_batch'])
+@pytest.mark.parametrize('order', ['rowmajor', 'colmajor'])
+@pytest.mark.parametrize('group', [1, 2, 4])
+def test_stream_covers_every_entry(policy, order, group):
+    A = sp.random(300, 260, density=0.05, format='csr', random_state=7, dtype=np.float32)
+    boo = S.csr_to_boo(A, cluster='random', target_nr=16, target_nc=24, small_block_policy=policy,
+                       nz_order=order, seed=3)
+    check_stream(A, boo, group=group)
+
+
+@pytest.mark.parametrize('nr,nc', [(32, 32), (64, 64), (8, 100), (100, 8)])
+@pytest.mark.parametrize('group', [1, 4])
+def test_stream_cuts_wide_and_tall_groups(nr, nc, group):
+    A = sp.random(400, 500, density=0.08, format='csr', random_state=1, dtype=np.float64)
+    boo = S.csr_to_boo(A, cluster='identity', target_nr=nr, target_nc=nc)
+    st = check_stream(A, boo, group=group)
+    assert st['ent_val'].dtype == np.float64
+
+
+def test_stream_dense_block_is_cut_between_rows():
+    A = sp.csr_matrix(np.arange(1, 32 * 32 + 1, dtype=np.float32).reshape(32, 32))
+    boo = S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32)
+    st = check_stream(A, boo)
+    tiles = st['tiles'].reshape(-1, 8)
+    assert len(tiles) == 8 and np.all(tiles[:, 1] & 0xff == 128)
+
+
+def test_stream_splits_heavy_items_and_long_rows():
+    A = sp.random(200, 3000, density=0.0005, format='lil', random_state=2, dtype=np.float32)
+    A[5, :] = 0.0
+    A[5, ::37] = 1.0                   # one entry per 32-column block: all remainder
+    A = A.tocsr()
+    boo = S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32)
+    for group in (1, 4):
+        st = check_stream(A, boo, max_item_nnz=10, long_thr=40, group=group)
+        assert st['n_slots'] > 0 and len(st['long_rows']) > 0
+
+
+def test_stream_empty_rows_get_a_tile():
+    A = sp.csr_matrix((70, 50), dtype=np.float32)
+    boo = S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32)
+    host = _host(boo)
+    st = _core.boo_stage(host, 4096, 256, 8, 1)
+    tiles = st['tiles'].reshape(-1, 8)
+    assert len(tiles) == 3 and np.all(tiles[:, 1] & 0xff == 0)   # 70 rows -> 3 slices
+
+
+def test_stream_config2_counts():
+    A, _ = M.make_config(2)
+    boo = S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32)
+    host = _host(boo)
+    st = _core.boo_stage(host, 4096, 256, 2048, 1)
+    tiles = st['tiles'].reshape(-1, 8)
+    nnz = tiles[:, 1] & 0xff
+    assert nnz.sum() == A.nnz and len(st['long_rows']) == 0
+    # 72,200 block tiles + one remainder tile per row group (8,192)
+    assert len(tiles) == 72200 + 8192
+    assert 2000 <= st['n_waves'] <= 2048 and st['n_slots'] == 0
+    # grouped by 4: the 27-point stencil's row groups share column groups, so
+    # a group of 4 loads far fewer X tiles than 4 separate row groups
+    st4 = _core.boo_stage(host, 4096, 256, 4096, 4)
+    t4 = st4['tiles'].reshape(-1, 8)
+    assert (t4[:, 1] & 0xff).sum() == A.nnz
+    steps = len(t4) // 4
+    assert steps < 0.55 * len(tiles)
+    # and the workgroups get near-equal numbers of steps (19 per group)
+    assert np.diff(st4['wave_tiles']).max() <= 38
+
+
+def test_stream_rejects_unsorted_blocks():
+    A = sp.random(64, 64, density=0.2, format='csr', random_state=0, dtype=np.float32)
+    boo = S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32)
+    host = _host(boo)
+    host['blk_row_grp'] = host['blk_row_grp'][::-1].copy()
+    with pytest.raises(ValueError, match='sorted'):
+        _core.boo_stage(host, 4096, 256, 8)
