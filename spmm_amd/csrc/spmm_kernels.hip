@@ -290,16 +290,20 @@ __device__ __forceinline__ void st_issue_near(StNear<T, F, VEC, NW>& nr, const S
     }
 }
 
-// Accumulate entries [j, e) of the LDS tile into this lane's row.
+// Accumulate entries [j, e) of the LDS tile into this lane's row.  The next
+// entry is read while the current one's X row is read and used, so each
+// iteration waits on one LDS round trip, not two.
 template <typename T, int F, int VEC, bool FULL>
-__device__ __forceinline__ void st_row(T (&acc)[F / VEC][VEC], int j, int e,
-                                       const NzEntry<T>* __restrict__ nzp,
+__device__ __forceinline__ void st_row(T (&acc)[F / VEC][VEC], int j, int e, const NzEntry<T>* nzp,
                                        const T* __restrict__ tile, int K, int fbase, int h) {
     typedef BooGeom<T, F, VEC> G;
+    if (j >= e) return;
+    NzEntry<T> ent = nzp[j];
 #pragma nounroll
     for (; j < e; ++j) {
-        const NzEntry<T> ent = nzp[j];
-        const T* xr = tile + ent.col * G::STRIDE + h * VEC;
+        const NzEntry<T> nxt = nzp[min(j + 1, e - 1)];
+        __builtin_amdgcn_sched_barrier(0);
+        const T* xr = tile + (int)(ent.col * (uint32_t)G::STRIDE) + h * VEC;
         T x[G::NQ][VEC];
 #pragma unroll
         for (int q = 0; q < G::NQ; ++q)
@@ -311,6 +315,7 @@ __device__ __forceinline__ void st_row(T (&acc)[F / VEC][VEC], int j, int e,
                 for (int u = 0; u < VEC; ++u) acc[q][u] += ent.val * x[q][u];
             }
         }
+        ent = nxt;
     }
 }
 
@@ -356,6 +361,25 @@ __device__ __forceinline__ void st_serial(uint64_t busy, int& rs0, int& rs1, NzE
     }
 }
 
+// Store an item's rows: lane (r, h) writes its half of row r (to Y, or to the
+// row of a partial slot).
+template <typename T, int F, int VEC, bool FULL>
+__device__ __forceinline__ void st_store(const StreamArgs<T>& a, const T (&acc)[F / VEC][VEC], int row,
+                                         int slot, int nrow, int b, int fbase) {
+    typedef BooGeom<T, F, VEC> G;
+    const int lane = threadIdx.x & 63;
+    const int h = lane & 1;
+    const int lr = lane >> 1;
+    const int K = a.K;
+    if (lr < nrow) {
+        T* out = slot < 0 ? a.Y + ((size_t)b * a.rows + row) * K + fbase + h * VEC
+                          : a.P + (((size_t)slot * a.batch + b) * ST_ROWS + lr) * K + fbase + h * VEC;
+#pragma unroll
+        for (int q = 0; q < G::NQ; ++q)
+            if (FULL || fbase + (2 * q + h) * VEC < K) store_vec<T, VEC>(out + 2 * q * VEC, acc[q]);
+    }
+}
+
 // LDS of one workgroup of WG waves: the shared X tile, double-buffered, and
 // per wave its entries, its serial-row sums and its column ids.
 template <typename T, int F, int VEC, int WG>
@@ -393,7 +417,7 @@ __device__ __forceinline__ void group_sync() {
 // partial slot of a split item).  Steps past the end of the stream load its
 // last tile (the data is never used) and store nothing.
 template <typename T, int F, int VEC, int D, int DF, int WG, bool FULL, bool A32>
-__global__ void __launch_bounds__(64 * WG) boo_stream_kernel(StreamArgs<T> a, int kt0) {
+__global__ void __launch_bounds__(64 * WG, 4) boo_stream_kernel(StreamArgs<T> a, int kt0) {
     typedef BooGeom<T, F, VEC> G;
     constexpr int NW = G::NST / WG;   // X staging instructions per wave
     static_assert(G::NST % WG == 0, "X tile does not split over the workgroup");
@@ -512,13 +536,7 @@ __global__ void __launch_bounds__(64 * WG) boo_stream_kernel(StreamArgs<T> a, in
         // (4) end of the item: store its rows
         if (real && ((mt.y >> 24) & ST_FLAG_LAST)) {
             const int nrow = (mt.y >> 16) & 0xff;
-            if (lr < nrow) {
-                T* out = slot < 0 ? a.Y + ((size_t)b * a.rows + row) * K + fbase + h * VEC
-                                  : a.P + (((size_t)slot * a.batch + b) * ST_ROWS + lr) * K + fbase + h * VEC;
-#pragma unroll
-                for (int q = 0; q < G::NQ; ++q)
-                    if (FULL || fbase + (2 * q + h) * VEC < K) store_vec<T, VEC>(out + 2 * q * VEC, acc[q]);
-            }
+            st_store<T, F, VEC, FULL>(a, acc, row, slot, nrow, b, fbase);
 #pragma unroll
             for (int q = 0; q < G::NQ; ++q)
 #pragma unroll
