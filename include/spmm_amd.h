@@ -78,8 +78,8 @@ const char* spmm_version(void);
  * listed in long_rows and summed by a split-row pass).  A slice heavier than
  * max_item_nnz is cut into several items: the first stores Y, the others
  * write partial sums to workspace slots that a fixup pass adds in slot order,
- * so results do not depend on scheduling.  Items are dealt to n_waves
- * persistent waves as contiguous ranges of near-equal cost.
+ * so results do not depend on scheduling.  Groups of slices (see group
+ * below) are dealt to workgroups as contiguous ranges of near-equal cost.
  * ------------------------------------------------------------------------- */
 
 /* Host copies of csr_to_boo's arrays, int32 indices, nz_idx row-major inside

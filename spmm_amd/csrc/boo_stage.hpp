@@ -20,11 +20,17 @@
 //   * a tile whose entries crowd into a few rows (a remainder row, say) is
 //     flagged to be computed one busy row at a time with lanes along K.
 //
-// A slice is one item unless its entries exceed max_item_nnz; then it is cut
-// at tile boundaries into several items: the first stores Y, the others write
-// partial sums to workspace slots that a fixup pass adds in slot order.
-// Items are dealt to n_waves persistent waves as contiguous ranges of roughly
-// equal cost.  Column ids of block tiles point into col_ids; those of
+// Up to `group` slices that share column chunks form a group, run by one
+// workgroup of `group` waves in lock step: step s stages one 32-column X tile
+// in LDS for all members, and each member (wave) adds its own tile of that
+// step.  Member streams therefore have equal length (padding tiles with no
+// entries fill the gaps) and equal column ids per step.
+//
+// A slice heavier than max_item_nnz sits alone in its group and is cut at tile
+// boundaries into several items: the first stores Y, the others write partial
+// sums to workspace slots that a fixup pass adds in slot order.  Groups are
+// dealt to workgroups as contiguous ranges of near-equal cost (an optimal
+// min-max split).  Column ids of block tiles point into col_ids; those of
 // remainder tiles are appended after it in the same array.
 #pragma once
 

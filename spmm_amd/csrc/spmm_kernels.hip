@@ -5,17 +5,19 @@
 // per sparse block and merge rows with global atomics into a memset Y --
 // kernels/boo_kernel.cu:410-595, kernels/pbr_kernel.cu:159-326):
 //
-//  * boo_stream_kernel -- persistent waves.  The matrix is staged on the host
-//    into a stream of tiles (<= 32 rows x 32 columns, <= 128 entries, row
-//    starts precomputed; see boo_stage.hpp) and each wave walks a contiguous
-//    range of whole items.  Lane (r, h) accumulates row r for half h of a
-//    64-feature tile in registers across the item's tiles (the BOO blocks,
-//    then the short remainder rows) and stores Y once.  Each tile's X column
-//    tile, entries and row range are loaded D tiles ahead into registers, and
-//    the column ids those loads need D tiles before that, so a step never
-//    waits on a load issued fewer than D steps earlier; the tile is then
-//    written to LDS (row stride padded by 32 bytes so neighbouring columns
-//    fall in distinct banks) and read back by the rows that use it.
+//  * boo_stream_kernel -- persistent workgroups of WG waves.  The matrix is
+//    staged on the host into tile streams (<= 32 rows x 32 columns, <= 128
+//    entries, row starts precomputed; see boo_stage.hpp): one stream per
+//    wave, the WG streams of a workgroup in lock step, step s of every member
+//    using the same 32 X columns.  Lane (r, h) of a wave accumulates row r of
+//    its 32-row slice for half h of a 64-feature tile in registers across the
+//    slice's tiles (the BOO blocks, then the short remainder rows) and stores
+//    Y once.  Each wave loads 32/WG of the step's X rows D steps ahead, and
+//    its tile's entries, row range and the column ids of the tile D steps
+//    later DF steps ahead, so a step never waits on a load issued in the
+//    same step; the X tile is then assembled in LDS (row stride padded by
+//    32 bytes so neighbouring columns fall in distinct banks), one barrier
+//    publishes it, and every member reads the columns its rows use.
 //  * boo_fixup_kernel -- for row slices too heavy for one item, adds the
 //    partial sums of the extra items into Y in slot order (deterministic).
 //  * rows_long_kernel -- remainder rows longer than the long-row threshold:

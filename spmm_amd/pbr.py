@@ -99,8 +99,10 @@ _CLASS = {(np.dtype(c.index_dtype), np.dtype(c.scalar_dtype)): c
 
 
 def _pinned(arr, device, dtype=None):
-    t = torch.from_numpy(np.ascontiguousarray(arr, dtype=dtype))
-    return t.pin_memory().to(device, non_blocking=True)
+    a = np.ascontiguousarray(arr, dtype=dtype)
+    if not a.flags.writeable:       # the builder's arrays are read-only views
+        a = a.copy()
+    return torch.from_numpy(a).pin_memory().to(device, non_blocking=True)
 
 
 def _pbr_to(self, device='cuda'):

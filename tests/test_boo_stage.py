@@ -178,3 +178,12 @@ def test_stream_rejects_unsorted_blocks():
     host['blk_row_grp'] = host['blk_row_grp'][::-1].copy()
     with pytest.raises(ValueError, match='sorted'):
         _core.boo_stage(host, 4096, 256, 8)
+
+
+def test_stream_rejects_bad_group():
+    A = sp.random(64, 64, density=0.2, format='csr', random_state=0, dtype=np.float32)
+    boo = S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32)
+    host = _host(boo)
+    for g in (0, 3, 8):
+        with pytest.raises(ValueError, match='group'):
+            _core.boo_stage(host, 4096, 256, 8, g)
