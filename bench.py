@@ -67,9 +67,10 @@ def time_steps(fns, steps, warmup, torch):
     return wall / steps * 1e3, e0.elapsed_time(e1) / steps
 
 
-def cpu_baseline(A, spec):
-    """The reference's own CPU BOO op (boo_batched_matmul_cpu, single thread),
-    compiled from its sources into oracle/_ref, on the same config."""
+def cpu_baseline(A, spec, cfg, fmt):
+    """The reference's own CPU op for the measured format
+    (boo_batched_matmul_cpu or pbr_batched_matmul_cpu, single thread), compiled
+    from its sources into oracle/_ref, on the same config."""
     import importlib
     import torch
     ref_dir = ROOT / 'oracle' / '_ref'
@@ -80,18 +81,24 @@ def cpu_baseline(A, spec):
     sys.path.insert(0, str(ROOT))
     from oracle import oracle as O
     K = spec['K']
-    rl = O.identity_labels(A.shape[0], 32)
-    b = ref.csr_to_boo(A.indptr, A.indices, A.data, A.shape[0], A.shape[1], rl, rl, 2, 4, 0)
+    if fmt == 'boo':
+        rl = O.identity_labels(A.shape[0], 32)
+        b = ref.csr_to_boo(A.indptr, A.indices, A.data, A.shape[0], A.shape[1], rl, rl, 2, 4, 0)
+        op = ref.boo_batched_matmul_cpu
+    else:
+        b = ref.csr_to_pbr(A.indptr, A.indices, A.data, A.shape[0], A.shape[1], 8, 8,
+                           spec.get('pbr_threshold', 4))
+        op = ref.pbr_batched_matmul_cpu
     from spmm_amd import matrices as M
     x = torch.from_numpy(M.dense_x(A.shape[1], K))
     nthreads = torch.get_num_threads()
     torch.set_num_threads(1)
     try:
-        ref.boo_batched_matmul_cpu(b, x)                    # warmup
+        op(b, x)                                            # warmup
         ts = []
         for _ in range(3):
             t0 = time.perf_counter()
-            ref.boo_batched_matmul_cpu(b, x)
+            op(b, x)
             ts.append(time.perf_counter() - t0)
     finally:
         torch.set_num_threads(nthreads)
@@ -107,7 +114,7 @@ def cpu_baseline(A, spec):
         pass
     return {'value': round(2.0 * A.nnz * K / t / 1e9, 3), 'unit': 'GFLOP/s', 'cores': 1,
             'kind': 'reference',
-            'sample': f'full config-2 matrix, K={K}: boo_batched_matmul_cpu, 1 warmup + median of 3 '
+            'sample': f'full config-{cfg} matrix, K={K}: {fmt}_batched_matmul_cpu, 1 warmup + median of 3 '
                       f'({t * 1e3:.0f} ms/call), single thread',
             'host_cpu': cpu_model, 'host_cores_available': len(os.sched_getaffinity(0))}
 
@@ -131,6 +138,40 @@ def calibrate_copy(torch):
         b.copy_(a)
     torch.cuda.synchronize()
     print(json.dumps({'calibrate_copy_bytes_each_way': 4 * n, 'reps': 5}))
+
+
+def bench_boo(S, A, K, Xs, Ys, dev, stream, args, O, torch):
+    """Time boo_matmul's entry point over rotating copies; returns (wall ms,
+    GPU ms per step, Python-API ms per call, parity ratio)."""
+    nrot = len(Xs)
+    boos = []
+    for _ in range(nrot):
+        t0 = time.perf_counter()
+        boos.append(S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32).to(dev))
+        d = boos[-1]._gpu_meta.desc
+        _log(f'BOO staged in {time.perf_counter() - t0:.1f} s: {d["n_tiles"]} tiles, {d["n_waves"]} waves, '
+             f'{d["n_crow"]} gather rows, {d["n_long"]} long rows, {d["n_splits"]} split slices')
+    ws_bytes = int(S._core.boo_workspace_bytes(boos[0]._gpu_meta.desc, 0, 1, K))
+    wss = [torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) for _ in range(nrot)]
+
+    def boo_step(i):
+        S._core.boo_matmul_gpu(boos[i]._gpu_meta.desc, 0, int(Xs[i].data_ptr()), int(Ys[i].data_ptr()),
+                               1, K, int(wss[i].data_ptr()), ws_bytes, int(stream))
+    boo_fns = [lambda i=i: boo_step(i) for i in range(nrot)]
+    # parity of the timed entry point against the fp64 product before timing
+    boo_step(0)
+    torch.cuda.synchronize()
+    ratio, ok = O.within_bound(Ys[0][0].cpu().numpy(), A, Xs[0].cpu().numpy(), 1e-5)
+    if not ok:
+        _log(f'PARITY FAILURE: max |err|/(|A||X|) = {ratio:.3e}')
+        sys.exit(1)
+    ms_wall, ms_ev_mean = time_steps(boo_fns, args.steps, args.warmup, torch)
+    api_fns = [lambda i=i: S.boo_matmul(boos[i], Xs[i]) for i in range(nrot)]
+    ms_api, _ = time_steps(api_fns, min(args.steps, 20), 3, torch)
+    _log(f'BOO: wall {ms_wall * 1e3:.1f} us/step, GPU (events over the timed region) '
+         f'{ms_ev_mean * 1e3:.1f} us/step; python API {ms_api * 1e3:.1f} us/call; '
+         f'parity ratio {ratio:.2e}')
+    return ms_wall, ms_ev_mean, ms_api, ratio
 
 
 def main():
@@ -165,42 +206,29 @@ def main():
     flops = 2.0 * nnz * K
     _log(f'config {args.config}: {spec["name"]} {A.shape} nnz={nnz} K={K} bytes_alg={balg}')
 
-    out = {}
-    Xs = [torch.from_numpy(M.dense_x(A.shape[1], K, seed=s)).cuda() for s in range(NROT)]
+    # Copies of matrix, X and Y rotate so that the 256 MB MALL cannot hold one
+    # step's data for the next; a config above 512 MB of compulsory traffic
+    # cannot stay in it anyway.
+    nrot = NROT if balg < 512e6 else 1
+    Xs = [torch.from_numpy(M.dense_x(A.shape[1], K, seed=s)).cuda() for s in range(nrot)]
     dev = torch.device('cuda', torch.cuda.current_device())
-
-    # ---- BOO (headline)
-    boos = [S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32).to(dev) for _ in range(NROT)]
-    Ys = [torch.empty((1, m, K), device=dev) for _ in range(NROT)]
-    ws_bytes = int(S._core.boo_workspace_bytes(boos[0]._gpu_meta.desc, 0, 1, K))
-    wss = [torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) for _ in range(NROT)]
+    Ys = [torch.empty((1, m, K), device=dev) for _ in range(nrot)]
     stream = torch.cuda.current_stream().cuda_stream
-
-    def boo_step(i):
-        S._core.boo_matmul_gpu(boos[i]._gpu_meta.desc, 0, int(Xs[i].data_ptr()), int(Ys[i].data_ptr()),
-                               1, K, int(wss[i].data_ptr()), ws_bytes, int(stream))
-    boo_fns = [lambda i=i: boo_step(i) for i in range(NROT)]
-    # parity of the timed entry point against the fp64 product before timing
-    boo_step(0)
-    torch.cuda.synchronize()
     from oracle import oracle as O
-    ratio, ok = O.within_bound(Ys[0][0].cpu().numpy(), A, Xs[0].cpu().numpy(), 1e-5)
-    if not ok:
-        _log(f'PARITY FAILURE: max |err|/(|A||X|) = {ratio:.3e}')
-        sys.exit(1)
-    ms_wall, ms_ev_mean = time_steps(boo_fns, args.steps, args.warmup, torch)
-    api_fns = [lambda i=i: S.boo_matmul(boos[i], Xs[i]) for i in range(NROT)]
-    ms_api, _ = time_steps(api_fns, min(args.steps, 20), 3, torch)
-    _log(f'BOO: wall {ms_wall * 1e3:.1f} us/step, GPU (events over the timed region) '
-         f'{ms_ev_mean * 1e3:.1f} us/step; python API {ms_api * 1e3:.1f} us/call; '
-         f'parity ratio {ratio:.2e}')
-    gbs = balg / (ms_ev_mean * 1e-3) / 1e9
+    has_boo = 'boo' in spec['formats']
+    run_pbr = 'pbr' in spec['formats'] and (not args.no_pbr or not has_boo)
+    fmt = 'boo' if has_boo else 'pbr'
+    ms_wall = ms_ev_mean = ms_api = ratio = None
+
+    # ---- BOO (headline when the config has it)
+    if has_boo:
+        ms_wall, ms_ev_mean, ms_api, ratio = bench_boo(S, A, K, Xs, Ys, dev, stream, args, O, torch)
 
     # ---- PBR on the same matrix
     pbr = {}
-    if 'pbr' in spec['formats'] and not args.no_pbr:
+    if run_pbr:
         thr = spec.get('pbr_threshold', 4)
-        pbrs = [S.csr_to_pbr(A, 8, 8, thr).to(dev) for _ in range(NROT)]
+        pbrs = [S.csr_to_pbr(A, 8, 8, thr).to(dev) for _ in range(nrot)]
 
         def pbr_step(i):
             S._core.pbr_matmul_gpu(pbrs[i]._gpu_meta.desc, 0, int(Xs[i].data_ptr()),
@@ -211,18 +239,26 @@ def main():
         if not pok:
             _log(f'PBR PARITY FAILURE: {pratio:.3e}')
             sys.exit(1)
-        p_wall, p_ev = time_steps([lambda i=i: pbr_step(i) for i in range(NROT)], args.steps,
+        p_wall, p_ev = time_steps([lambda i=i: pbr_step(i) for i in range(nrot)], args.steps,
                                      args.warmup, torch)
         pbr = {'ms_per_step': round(p_wall, 5), 'kernel_ms_mean': round(p_ev, 5),
                'gflops': round(flops / (p_wall * 1e-3) / 1e9, 2),
                'hbm_gbs': round(balg / (p_ev * 1e-3) / 1e9, 1),
                'hbm_frac': round(balg / (p_ev * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
         _log(f'PBR: wall {p_wall * 1e3:.1f} us/step, kernel {p_ev * 1e3:.1f} us')
+        if not has_boo:                    # PBR is the measured path of this config
+            ms_wall, ms_ev_mean, ratio = p_wall, p_ev, pratio
 
-    workload = f'cfg{args.config}_{spec["name"]}_boo_identity32_K{K}'
-    cpu = None if args.no_cpu_baseline else cpu_baseline(A, spec)
+    gbs = balg / (ms_ev_mean * 1e-3) / 1e9
+    if has_boo:
+        workload = f'cfg{args.config}_{spec["name"]}_boo_identity32_K{K}'
+        fmt_desc = 'BOO identity 32x32, remainder policy (threshold 4)'
+    else:
+        workload = f'cfg{args.config}_{spec["name"]}_pbr8x8_thr{spec.get("pbr_threshold", 4)}_K{K}'
+        fmt_desc = f'PBR 8x8, min_nnz_per_block {spec.get("pbr_threshold", 4)}'
+    cpu = None if args.no_cpu_baseline else cpu_baseline(A, spec, args.config, fmt)
     out = {
-        'metric': 'SpMM GFLOP/s (2*nnz*K/t), boo_matmul; HBM GB/s of algorithmic bytes vs 8 TB/s',
+        'metric': f'SpMM GFLOP/s (2*nnz*K/t), {fmt}_matmul; HBM GB/s of algorithmic bytes vs 8 TB/s',
         'value': round(flops / (ms_wall * 1e-3) / 1e9, 2),
         'unit': 'GFLOP/s',
         'n_gpus': 1,
@@ -235,14 +271,13 @@ def main():
         'dtype': 'f32',
         'data': 'synthetic',
         'config': {'workload': workload, 'matrix': spec['name'], 'rows': m, 'nnz': nnz, 'K': K,
-                   'format': 'BOO identity 32x32, remainder policy (threshold 4)',
-                   'bytes_alg': balg, 'rotation_copies': NROT},
+                   'format': fmt_desc, 'bytes_alg': balg, 'rotation_copies': nrot},
         'hbm_gbs': round(balg / (ms_wall * 1e-3) / 1e9, 1),
         'roofline': {'bound': 'hbm', 'achieved': round(gbs, 1), 'peak': PEAK_HBM_GBS, 'unit': 'GB/s',
                      'frac': round(gbs / PEAK_HBM_GBS, 4),
                      'traffic': (traffic_from_profiles(workload) or {}).get('bytes_per_launch')},
         'kernel_us_mean': round(ms_ev_mean * 1e3, 2),
-        'python_api_us_per_call': round(ms_api * 1e3, 2),
+        'python_api_us_per_call': round(ms_api * 1e3, 2) if ms_api is not None else None,
         'pbr': pbr,
         'cpu_baseline': cpu,
     }

@@ -80,6 +80,10 @@ const char* spmm_version(void);
  * write partial sums to workspace slots that a fixup pass adds in slot order,
  * so results do not depend on scheduling.  Groups of slices (see group
  * below) are dealt to workgroups as contiguous ranges of near-equal cost.
+ * Empty slices, and slices whose nonzeros use each distinct column fewer than
+ * min_reuse times on average (scattered columns, where staging X tiles cannot
+ * pay), leave the tile stream: their rows become a CSR with global columns that a
+ * row-wise gather pass computes and stores whole.
  * ------------------------------------------------------------------------- */
 
 /* Host copies of csr_to_boo's arrays, int32 indices, nz_idx row-major inside
@@ -105,28 +109,34 @@ typedef struct spmm_boo_host {
 typedef struct spmm_boo_stage spmm_boo_stage;  /* opaque, host memory */
 
 typedef struct spmm_boo_stage_info {
-    int64_t n_tiles, n_ent, n_tcols, n_splits, n_long;
+    int64_t n_tiles, n_ent, n_tcols, n_splits, n_long, n_crow, n_cnz;
     int32_t n_slots, n_waves, group;
 } spmm_boo_stage_info;
 
 /* group (1, 2 or 4): slices that share column chunks are put together, up to
  * group of them, and walk one tile stream in lockstep -- the waves of one
  * workgroup, each owning one slice, load each X tile once between them.
- * n_waves is rounded down to a multiple of group. */
+ * n_waves is rounded down to a multiple of group.  min_reuse: slices whose
+ * nonzeros use each distinct column fewer than min_reuse times on average,
+ * and empty slices, go to the gather pass (0: none does; 1.5 is the default
+ * of the Python layer). */
 int spmm_boo_stage_create(const spmm_boo_host* H, int32_t max_item_nnz, int32_t long_threshold,
-                          int32_t n_waves, int32_t group, spmm_boo_stage** out);
+                          int32_t n_waves, int32_t group, float min_reuse, spmm_boo_stage** out);
 int spmm_boo_stage_sizes(const spmm_boo_stage* st, spmm_boo_stage_info* info);
 /* Host output arrays, sized from spmm_boo_stage_sizes:
  *   tiles [n_tiles*8] int32: ent_off, nnz | nc<<8 | nr<<16 | flags<<24, cid_off, row_off,
  *                            slot (-1: the item stores Y, else its partial slot), 0, 0, 0
  *   tile_rs [n_tiles*33] uint16, ent_val [n_ent] (dtype), ent_col [n_ent] uint8,
  *   tcols [n_tcols] int32, splits [n_splits*4] int32, long_rows [n_long] int32,
- *   wave_tiles [n_waves+1] int32.
+ *   wave_tiles [n_waves+1] int32,
+ *   crow_ptr [n_crow+1] int32, crow_id [n_crow] int32, ccol [n_cnz] int32, cval [n_cnz] (dtype):
+ *   the rows of the gather pass (Y row ids, their entries with global columns).
  * Every tile's entries start at an even index (odd tiles are followed by a
  * zero entry). */
 int spmm_boo_stage_copy(const spmm_boo_stage* st, int32_t* tiles, uint16_t* tile_rs,
                         void* ent_val, uint8_t* ent_col, int32_t* tcols, int32_t* splits,
-                        int32_t* long_rows, int32_t* wave_tiles);
+                        int32_t* long_rows, int32_t* wave_tiles, int32_t* crow_ptr,
+                        int32_t* crow_id, int32_t* ccol, void* cval);
 void spmm_boo_stage_destroy(spmm_boo_stage* st);
 
 /* Device descriptor: the staged arrays plus row_ids and the remainder CSR
@@ -148,6 +158,11 @@ typedef struct spmm_boo_desc {
     const int32_t* splits;       /* [n_splits*4]: row_off, nr, slot_begin, slot_end */
     int32_t n_long;
     const int32_t* long_rows;    /* [n_long] */
+    int32_t n_crow;              /* rows of the gather pass (0: none) */
+    const int32_t* crow_ptr;     /* [n_crow+1] */
+    const int32_t* crow_id;      /* [n_crow] */
+    const int32_t* ccol;         /* [n_cnz] (may be null when n_cnz is 0) */
+    const void* cval;            /* [n_cnz] (may be null when n_cnz is 0) */
     const int32_t* rem_indptr;   /* [rows+1] */
     const int32_t* rem_col_ind;
     const void* rem_vals;

@@ -42,6 +42,7 @@ MAX_ITEM_NNZ = 4096        # a heavier 32-row slice is cut into several work ite
 LONG_ROW_THRESHOLD = 256   # longer remainder rows go to the split-row pass
 WAVES_PER_CU = 16          # persistent waves per compute unit (4 per SIMD at <= 128 VGPRs)
 GROUP = 4                  # slices sharing X tiles per workgroup
+MIN_COL_REUSE = 1.5        # slices using each column less often go to the gather pass
 
 
 class BooNzOrder(enum.IntEnum):
@@ -215,7 +216,8 @@ def _boo_to(self, device='cuda'):
         'nz_val': np.ascontiguousarray(k_val),
         'rem_indptr': k_rem_indptr, 'rem_col_ind': k_rem_col, 'rem_vals': k_rem_val,
     }
-    stage = core.boo_stage(host, MAX_ITEM_NNZ, LONG_ROW_THRESHOLD, max(GROUP, n_cu * WAVES_PER_CU), GROUP)
+    stage = core.boo_stage(host, MAX_ITEM_NNZ, LONG_ROW_THRESHOLD, max(GROUP, n_cu * WAVES_PER_CU), GROUP,
+                           MIN_COL_REUSE)
 
     # Field names and dtypes of the reference's _gpu_meta (boo.py:72-92) ...
     meta = types.SimpleNamespace(
@@ -236,11 +238,11 @@ def _boo_to(self, device='cuda'):
         tail_col=_pinned(d['tail_col'], device, i32),
         tail_val=_pinned(d['tail_val'], device),
     )
-    # ... plus the kernel's tile stream (spmm_boo_stage_*) and the remainder
-    # CSR with the tail folded in, read by the long-row pass.
+    # ... plus the kernel's tile stream and gather rows (spmm_boo_stage_*) and
+    # the remainder CSR with the tail folded in, read by the long-row pass.
     meta.stage = types.SimpleNamespace(**{k: _pinned(stage[k], device) for k in (
         'tiles', 'tile_rs', 'ent_val', 'ent_col', 'tcols', 'splits', 'long_rows',
-        'wave_tiles')})
+        'wave_tiles', 'crow_ptr', 'crow_id', 'ccol', 'cval')})
     if self.tail_nnz():
         meta.k_rem_indptr = _pinned(k_rem_indptr, device)
         meta.k_rem_col_ind = _pinned(k_rem_col, device)
@@ -260,6 +262,8 @@ def _boo_to(self, device='cuda'):
         'wave_tiles': p(g.wave_tiles),
         'n_slots': int(stage['n_slots']), 'n_splits': int(stage['n_splits']), 'splits': p(g.splits),
         'n_long': int(stage['n_long']), 'long_rows': p(g.long_rows),
+        'n_crow': int(stage['n_crow']), 'crow_ptr': p(g.crow_ptr), 'crow_id': p(g.crow_id),
+        'ccol': p(g.ccol), 'cval': p(g.cval),
         'rem_indptr': p(meta.k_rem_indptr), 'rem_col_ind': p(meta.k_rem_col_ind),
         'rem_vals': p(meta.k_rem_vals),
     }

@@ -57,6 +57,8 @@ constexpr int SERIAL_MAX_BUSY = 8;    // busy rows a serial tile may have
 constexpr long long COST_STEP = 256;
 constexpr long long COST_ITEM = 512;
 
+
+
 struct Staged {
     // [n_tiles][8]: ent_off, nnz|nc<<8|nr<<16|flags<<24, cid_off, row_off, slot, 0, 0, 0
     // (slot -1: the item stores Y; otherwise its partial slot)
@@ -68,6 +70,11 @@ struct Staged {
     std::vector<int32_t> splits;     // [n_splits][4]: row_off, nr, slot_begin, slot_end
     std::vector<int32_t> long_rows;  // rows whose remainder exceeds long_threshold
     std::vector<int32_t> wave_tiles; // [n_waves+1]
+    // rows of the gather pass: Y row ids, CSR of their entries (global columns)
+    std::vector<int32_t> crow_ptr;   // [n_crow+1]
+    std::vector<int32_t> crow_id;    // [n_crow]
+    std::vector<int32_t> ccol;       // [n_cnz]
+    std::vector<char> cval;          // [n_cnz] values (float or double bytes)
     int32_t n_slots = 0;
     int32_t n_waves = 0;
     int32_t group = 1;               // waves per workgroup sharing X tiles
@@ -97,18 +104,26 @@ public:
         const T* rem_vals;
     };
 
-    Builder(const In& in, int max_item_nnz, int long_threshold, int n_waves, int group)
+    // min_reuse: a slice whose nonzeros use each of their distinct columns
+    // fewer than min_reuse times on average (scattered columns: a permuted or
+    // power-law matrix) gains nothing from staging X tiles, and its rows go to
+    // the row-wise gather pass, as do empty slices; 0 keeps every slice in
+    // the tile stream.
+    Builder(const In& in, int max_item_nnz, int long_threshold, int n_waves, int group, float min_reuse)
         : in_(in), max_item_nnz_(max_item_nnz), long_threshold_(long_threshold),
-          want_waves_(n_waves), G_(group) {}
+          want_waves_(n_waves), G_(group), min_reuse_(min_reuse) {}
 
     void run(Staged& S) {
         S = Staged();
         S.group = G_;
         S.tcols.assign(in_.col_ids, in_.col_ids + in_.cols);
         collect_slices(S);
+        classify_slices();
         make_groups();
         for (size_t g = 0; g < groups_.size(); ++g) build_group_steps(S, g);
+        split_heavy(S);
         deal_and_emit(S);
+        emit_csr(S);
     }
 
 private:
@@ -122,6 +137,7 @@ private:
         size_t c0, c1;  // chunks in chunks_
         size_t r0, r1;  // remainder entries in pool_ (lc = 0; column in rcol_)
         long long nnz;
+        bool csr;       // rows go to the gather pass, not the tile stream
     };
     // ---- one step of a group: one X tile, each member's entries in it
     struct Step {
@@ -136,6 +152,7 @@ private:
         int n_members;
         size_t s0, s1;  // steps in steps_
         long long cost;
+        int slot;       // -1: stores Y; else the partial slot of an item of a split slice
     };
 
     void collect_slices(Staged& S) {
@@ -156,6 +173,7 @@ private:
                 sl.row_off = r0 + s0;
                 sl.c0 = chunks_.size();
                 sl.nnz = 0;
+                sl.csr = false;
                 for (int b = bb; b < be; ++b) {
                     const int cg = in_.blk_col_grp[b];
                     if (cg < 0 || cg >= in_.n_col_groups) throw std::invalid_argument("blk_col_grp out of range");
@@ -221,6 +239,65 @@ private:
         rcol_.resize(pool_.size());
     }
 
+    // Global column of a pool_ entry of slice chunk c (block) or remainder.
+    int32_t ent_col_of(size_t e, const Chunk* c) const {
+        return c ? in_.col_ids[c->cid_off + pool_[e].lc] : rcol_[e];
+    }
+
+    // Send empty slices and slices with scattered columns to the gather pass.
+    // A slice heavier than max_item_nnz stays in the stream, where it is cut
+    // into items that run in parallel.
+    void classify_slices() {
+        std::vector<int32_t> cols;
+        if (!(min_reuse_ > 0.0f)) return;
+        for (Slice& sl : slices_) {
+            if (sl.nnz == 0) {
+                sl.csr = true;
+                continue;
+            }
+            if (sl.nnz > max_item_nnz_) continue;
+            cols.clear();
+            for (size_t c = sl.c0; c < sl.c1; ++c)
+                for (size_t e = chunks_[c].e0; e < chunks_[c].e1; ++e) cols.push_back(ent_col_of(e, &chunks_[c]));
+            for (size_t e = sl.r0; e < sl.r1; ++e) cols.push_back(rcol_[e]);
+            std::sort(cols.begin(), cols.end());
+            const long long distinct = std::unique(cols.begin(), cols.end()) - cols.begin();
+            sl.csr = (double)sl.nnz < (double)min_reuse_ * (double)distinct;
+        }
+    }
+
+    // The gather pass's rows: every row of every slice sent there, with its
+    // block entries (in block order) and then its short remainder entries.
+    void emit_csr(Staged& S) {
+        struct RE {
+            int32_t lr, col;
+            int32_t src;
+            int32_t from_rem;
+        };
+        std::vector<RE> v;
+        S.crow_ptr.assign(1, 0);
+        for (const Slice& sl : slices_) {
+            if (!sl.csr) continue;
+            v.clear();
+            for (size_t c = sl.c0; c < sl.c1; ++c)
+                for (size_t e = chunks_[c].e0; e < chunks_[c].e1; ++e)
+                    v.push_back(RE{pool_[e].lr, ent_col_of(e, &chunks_[c]), pool_[e].src, 0});
+            for (size_t e = sl.r0; e < sl.r1; ++e) v.push_back(RE{pool_[e].lr, rcol_[e], pool_[e].src, 1});
+            std::stable_sort(v.begin(), v.end(), [](const RE& a, const RE& b) { return a.lr < b.lr; });
+            size_t k = 0;
+            for (int lr = 0; lr < sl.nr; ++lr) {
+                S.crow_id.push_back(in_.row_ids[sl.row_off + lr]);
+                for (; k < v.size() && v[k].lr == lr; ++k) {
+                    S.ccol.push_back(v[k].col);
+                    const T x = v[k].from_rem ? in_.rem_vals[v[k].src] : in_.nz_val[v[k].src];
+                    const char* p = reinterpret_cast<const char*>(&x);
+                    S.cval.insert(S.cval.end(), p, p + sizeof(T));
+                }
+                S.crow_ptr.push_back((int32_t)S.ccol.size());
+            }
+        }
+    }
+
     // Slices that share column chunks go into one group (up to G): a group
     // loads each chunk's X tile once for all its members.  Greedy: take the
     // first free slice, then repeatedly the free slice with the most chunks in
@@ -235,12 +312,14 @@ private:
         std::sort(kv.begin(), kv.end());
         auto heavy = [&](int i) { return slices_[i].nnz > max_item_nnz_; };
         std::vector<char> used(ns, 0);
+        for (int i = 0; i < ns; ++i) used[i] = slices_[i].csr;
         std::vector<int> score(ns, 0), touched;
         std::vector<int> keys;
         int fill = 0;
         for (int i = 0; i < ns; ++i) {
             if (used[i]) continue;
             Group g{};
+            g.slot = -1;
             g.members[0] = i;
             g.n_members = 1;
             used[i] = 1;
@@ -431,6 +510,49 @@ private:
     // groups, its member's tile of every step.  A slice alone in its group is
     // cut into items of at most max_item_nnz entries (the first stores Y, the
     // others partial slots).
+    // A slice heavier than max_item_nnz (alone in its group) becomes several
+    // items, each a group of its own so that different workgroups run them:
+    // a run of its steps with at most max_item_nnz entries (or one step).
+    // The first item stores Y, the others write partial slots that the fixup
+    // pass adds in slot order.
+    void split_heavy(Staged& S) {
+        std::vector<Group> out;
+        out.reserve(groups_.size());
+        for (const Group& g : groups_) {
+            const Slice& sl = slices_[g.members[0]];
+            if (g.n_members != 1 || sl.nnz <= max_item_nnz_) {
+                out.push_back(g);
+                continue;
+            }
+            const int slot_begin = S.n_slots;
+            size_t a = g.s0;
+            long long nnz = 0;
+            for (size_t st = g.s0; st < g.s1; ++st) {
+                const Piece& pc = pieces_[steps_[st].m0];
+                nnz += (long long)(pc.e1 - pc.e0);
+                bool end = st + 1 == g.s1;
+                if (!end) {
+                    const Piece& nx = pieces_[steps_[st + 1].m0];
+                    end = nnz + (long long)(nx.e1 - nx.e0) > max_item_nnz_;
+                }
+                if (!end) continue;
+                Group it = g;
+                it.s0 = a;
+                it.s1 = st + 1;
+                it.slot = a == g.s0 ? -1 : S.n_slots++;
+                it.cost = COST_ITEM + (long long)(it.s1 - it.s0) * COST_STEP + nnz;
+                out.push_back(it);
+                a = st + 1;
+                nnz = 0;
+            }
+            if (S.n_slots > slot_begin) {
+                const int32_t sp4[4] = {sl.row_off, sl.nr, slot_begin, S.n_slots};
+                S.splits.insert(S.splits.end(), sp4, sp4 + 4);
+            }
+        }
+        groups_.swap(out);
+    }
+
     void deal_and_emit(Staged& S) {
         const int ng = (int)groups_.size();
         int nwg = std::max(1, std::min(std::max(want_waves_ / G_, 1), ng));
@@ -479,30 +601,11 @@ private:
                     const bool real = m < g.n_members;
                     const Slice* sl = real ? &slices_[g.members[m]] : nullptr;
                     const int row_off = real ? sl->row_off : 0, nr = real ? sl->nr : 0;
-                    // items of this member: cut at max_item_nnz when alone
-                    int slot = -1;
-                    long long nnz = 0;
-                    const int slot_begin = S.n_slots;
                     for (size_t st = g.s0; st < g.s1; ++st) {
                         const Step& sp = steps_[st];
                         const Piece& pc = pieces_[sp.m0 + m];
-                        const long long tn = (long long)(pc.e1 - pc.e0);
-                        uint32_t flags = 0;
-                        if (st + 1 == g.s1) flags |= FLAG_LAST;
-                        if (real && g.n_members == 1 && st + 1 < g.s1) {
-                            const Piece& nx = pieces_[steps_[st + 1].m0 + m];
-                            if (nnz + tn + (long long)(nx.e1 - nx.e0) > max_item_nnz_ && nnz + tn > 0) flags |= FLAG_LAST;
-                        }
-                        emit_tile(S, real ? pc : Piece{0, 0}, sp.cid_off, sp.nc, row_off, nr, flags, slot);
-                        nnz += tn;
-                        if ((flags & FLAG_LAST) && st + 1 < g.s1) {  // next item of a split slice
-                            slot = S.n_slots++;
-                            nnz = 0;
-                        }
-                    }
-                    if (S.n_slots > slot_begin) {
-                        const int32_t sp4[4] = {row_off, nr, slot_begin, S.n_slots};
-                        S.splits.insert(S.splits.end(), sp4, sp4 + 4);
+                        const uint32_t flags = st + 1 == g.s1 ? FLAG_LAST : 0u;
+                        emit_tile(S, real ? pc : Piece{0, 0}, sp.cid_off, sp.nc, row_off, nr, flags, real ? g.slot : -1);
                     }
                 }
                 S.wave_tiles.push_back((int32_t)S.n_tiles());
@@ -519,6 +622,7 @@ private:
 
     In in_;
     int max_item_nnz_, long_threshold_, want_waves_, G_;
+    float min_reuse_;
     std::vector<Ent> pool_, tent_;
     std::vector<int32_t> rcol_, colx_;
     std::vector<Chunk> chunks_;

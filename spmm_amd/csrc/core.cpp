@@ -286,6 +286,11 @@ spmm_boo_desc boo_desc(const py::dict& d) {
     A.splits = reinterpret_cast<const int32_t*>(P(d, "splits"));
     A.n_long = d["n_long"].cast<int32_t>();
     A.long_rows = reinterpret_cast<const int32_t*>(P(d, "long_rows"));
+    A.n_crow = d["n_crow"].cast<int32_t>();
+    A.crow_ptr = reinterpret_cast<const int32_t*>(P(d, "crow_ptr"));
+    A.crow_id = reinterpret_cast<const int32_t*>(P(d, "crow_id"));
+    A.ccol = reinterpret_cast<const int32_t*>(P(d, "ccol"));
+    A.cval = reinterpret_cast<const void*>(P(d, "cval"));
     A.rem_indptr = reinterpret_cast<const int32_t*>(P(d, "rem_indptr"));
     A.rem_col_ind = reinterpret_cast<const int32_t*>(P(d, "rem_col_ind"));
     A.rem_vals = reinterpret_cast<const void*>(P(d, "rem_vals"));
@@ -295,7 +300,7 @@ spmm_boo_desc boo_desc(const py::dict& d) {
 // Host staging of a BOO matrix into the kernel's tile stream (spmm_boo_stage_*).
 // h: the BOO arrays as int32 / uint8 / uint16 numpy arrays plus the sizes.
 py::dict boo_stage(const py::dict& h, int32_t max_item_nnz, int32_t long_threshold, int32_t n_waves,
-                   int32_t group) {
+                   int32_t group, float min_reuse) {
     auto arr = [&](const char* k) { return h[k].cast<py::array>(); };
     const py::array nz_val = arr("nz_val"), rem_vals = arr("rem_vals");
     const bool f64 = is_f64(nz_val);
@@ -323,17 +328,22 @@ py::dict boo_stage(const py::dict& h, int32_t max_item_nnz, int32_t long_thresho
     if (!(nz_val.flags() & py::array::c_style) || !(rem_vals.flags() & py::array::c_style))
         throw std::invalid_argument("values must be contiguous");
     spmm_boo_stage* st = nullptr;
-    raise_status(spmm_boo_stage_create(&H, max_item_nnz, long_threshold, n_waves, group, &st));
+    raise_status(spmm_boo_stage_create(&H, max_item_nnz, long_threshold, n_waves, group, min_reuse, &st));
     spmm_boo_stage_info inf{};
     spmm_boo_stage_sizes(st, &inf);
     std::vector<int32_t> tiles((size_t)inf.n_tiles * 8), tcols((size_t)inf.n_tcols),
-        splits((size_t)inf.n_splits * 4), longr((size_t)inf.n_long), wt((size_t)inf.n_waves + 1);
+        splits((size_t)inf.n_splits * 4), longr((size_t)inf.n_long), wt((size_t)inf.n_waves + 1),
+        crp((size_t)inf.n_crow + 1), cri((size_t)inf.n_crow), ccol((size_t)inf.n_cnz);
     std::vector<uint16_t> rs((size_t)inf.n_tiles * 33);
     std::vector<uint8_t> ecol((size_t)inf.n_ent);
     py::array ev = f64 ? py::array(py::array_t<double>((py::ssize_t)inf.n_ent))
                        : py::array(py::array_t<float>((py::ssize_t)inf.n_ent));
+    py::array cv = f64 ? py::array(py::array_t<double>((py::ssize_t)inf.n_cnz))
+                       : py::array(py::array_t<float>((py::ssize_t)inf.n_cnz));
     const int rc = spmm_boo_stage_copy(st, tiles.data(), rs.data(), inf.n_ent ? ev.mutable_data() : nullptr,
-                                       ecol.data(), tcols.data(), splits.data(), longr.data(), wt.data());
+                                       ecol.data(), tcols.data(), splits.data(), longr.data(), wt.data(),
+                                       crp.data(), cri.data(), ccol.data(),
+                                       inf.n_cnz ? cv.mutable_data() : nullptr);
     spmm_boo_stage_destroy(st);
     raise_status(rc);
     py::dict d;
@@ -345,6 +355,11 @@ py::dict boo_stage(const py::dict& h, int32_t max_item_nnz, int32_t long_thresho
     d["splits"] = give(std::move(splits));
     d["long_rows"] = give(std::move(longr));
     d["wave_tiles"] = give(std::move(wt));
+    d["crow_ptr"] = give(std::move(crp));
+    d["crow_id"] = give(std::move(cri));
+    d["ccol"] = give(std::move(ccol));
+    d["cval"] = cv;
+    d["n_crow"] = inf.n_crow;
     d["n_tiles"] = inf.n_tiles;
     d["n_slots"] = inf.n_slots;
     d["n_splits"] = inf.n_splits;
@@ -419,7 +434,7 @@ PYBIND11_MODULE(_core, m) {
                          batch, K);
     });
     m.def("boo_stage", &boo_stage, py::arg("h"), py::arg("max_item_nnz"), py::arg("long_threshold"),
-          py::arg("n_waves"), py::arg("group") = 1);
+          py::arg("n_waves"), py::arg("group") = 1, py::arg("min_reuse") = 0.0f);
     m.def("boo_workspace_bytes", &boo_workspace_bytes);
     m.def("boo_matmul_gpu", &boo_matmul_gpu);
     m.def("pbr_matmul_gpu", &pbr_matmul_gpu);

@@ -294,18 +294,20 @@ __device__ __forceinline__ void st_issue_near(StNear<T, F, VEC, NW>& nr, const S
 
 // Accumulate entries [j, e) of the LDS tile into this lane's row.  The next
 // entry is read while the current one's X row is read and used, so each
-// iteration waits on one LDS round trip, not two.
+// iteration waits on one LDS round trip, not two.  The read-ahead reaches
+// nzp[e] at most, which is inside the workgroup's LDS (e <= ST_ENT + ST_SYN,
+// and nzp is followed by colbuf).  Addresses are formed in 32 bits in the
+// LDS address space (one 24-bit multiply-add per entry).
 template <typename T, int F, int VEC, bool FULL>
 __device__ __forceinline__ void st_row(T (&acc)[F / VEC][VEC], int j, int e, const NzEntry<T>* nzp,
                                        const T* __restrict__ tile, int K, int fbase, int h) {
     typedef BooGeom<T, F, VEC> G;
     if (j >= e) return;
-    NzEntry<T> ent = nzp[j];
-#pragma nounroll
-    for (; j < e; ++j) {
-        const NzEntry<T> nxt = nzp[min(j + 1, e - 1)];
-        __builtin_amdgcn_sched_barrier(0);
-        const T* xr = tile + (int)(ent.col * (uint32_t)G::STRIDE) + h * VEC;
+    typedef __attribute__((address_space(3))) const char lds_char;
+    typedef __attribute__((address_space(3))) const T lds_t;
+    lds_char* tb = (lds_char*)(tile) + h * VEC * (int)sizeof(T);
+    auto entry = [&](const NzEntry<T>& ent) {
+        const T* xr = (const T*)(lds_t*)(tb + __umul24(ent.col, (uint32_t)(G::STRIDE * sizeof(T))));
         T x[G::NQ][VEC];
 #pragma unroll
         for (int q = 0; q < G::NQ; ++q)
@@ -317,6 +319,13 @@ __device__ __forceinline__ void st_row(T (&acc)[F / VEC][VEC], int j, int e, con
                 for (int u = 0; u < VEC; ++u) acc[q][u] += ent.val * x[q][u];
             }
         }
+    };
+    NzEntry<T> ent = nzp[j];
+#pragma nounroll
+    for (; j < e; ++j) {
+        const NzEntry<T> nxt = nzp[j + 1];
+        __builtin_amdgcn_sched_barrier(0);
+        entry(ent);
         ent = nxt;
     }
 }
@@ -436,6 +445,7 @@ __global__ void __launch_bounds__(64 * WG, 4) boo_stream_kernel(StreamArgs<T> a,
     const int b = blockIdx.z;
     const T* Xb = a.X + (size_t)b * a.cols * K;
     const int t0 = a.wave_tiles[w], t1 = a.wave_tiles[w + 1];
+    if (t0 >= t1) return;  // uniform per workgroup: its streams have equal lengths
     const int tl = t1 - 1;
     auto cl = [tl](int t) { return min(t, tl); };
     int* colbuf = L.colbuf[wv];
@@ -577,6 +587,66 @@ __global__ void __launch_bounds__(256) boo_fixup_kernel(const int* __restrict__ 
         for (int sl = sb; sl < se; ++sl) acc += P[(((size_t)sl * batch + b) * ST_ROWS + lr) * K + f];
         *y = acc;
     }
+}
+
+// ---------------------------------------------------------------------------
+// BOO gather pass: the rows of slices whose columns are too scattered for X
+// tiles to pay (each column used about once).  LPR lanes per row, VEC features
+// each (blockIdx.y picks the feature tile); a workgroup of 256 threads covers
+// 256 / LPR rows.  The row's entries are read LPR at a time, one per lane
+// (coalesced), and handed to the row's lanes by a shuffle; each entry's slice
+// of its X row is then gathered straight from memory, U entries at a time so
+// that U gathers are in flight.  The row is stored once (plain stores).
+// ---------------------------------------------------------------------------
+
+template <typename T, int VEC, int LPR>
+__global__ void __launch_bounds__(256) boo_rows_kernel(const int* __restrict__ crow_ptr,
+                                                       const int* __restrict__ crow_id,
+                                                       const int* __restrict__ ccol,
+                                                       const T* __restrict__ cval, int n_crow,
+                                                       const T* __restrict__ X, T* __restrict__ Y,
+                                                       int rows, int cols, int K) {
+    constexpr int RPB = 256 / LPR;
+    constexpr int U = 8;
+    static_assert(LPR >= 1 && LPR <= 64 && (LPR & (LPR - 1)) == 0, "LPR must be a power of two <= 64");
+    const int r = xcd_remap(blockIdx.x, gridDim.x) * RPB + (int)threadIdx.x / LPR;
+    if (r >= n_crow) return;  // no barriers below
+    const int l = threadIdx.x % LPR;
+    const int gbase = (threadIdx.x & 63) & ~(LPR - 1);  // first lane of this row in the wave
+    const int f = (int)blockIdx.y * (LPR * VEC) + l * VEC;
+    const bool fok = f < K;  // K is a multiple of VEC
+    const int b = blockIdx.z;
+    const T* Xb = X + (size_t)b * cols * K;
+    const int p0 = crow_ptr[r], p1 = crow_ptr[r + 1];
+    T acc[VEC];
+#pragma unroll
+    for (int u = 0; u < VEC; ++u) acc[u] = T(0);
+    for (int p = p0; p < p1; p += LPR) {
+        const int n = min(LPR, p1 - p);
+        // lanes past the row's end repeat its first entry with value 0
+        const int c = ccol[p + (l < n ? l : 0)];
+        const T v = l < n ? cval[p + l] : T(0);
+        for (int i0 = 0; i0 < n; i0 += U) {
+            int ci[U];
+            T vi[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int src = gbase + min(i0 + u, LPR - 1);
+                ci[u] = __shfl(c, src);
+                vi[u] = i0 + u < n ? __shfl(v, src) : T(0);
+            }
+            if (fok) {
+                T x[U][VEC];
+#pragma unroll
+                for (int u = 0; u < U; ++u) load_vec<T, VEC>(Xb + (size_t)ci[u] * K + f, x[u]);
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+#pragma unroll
+                    for (int e = 0; e < VEC; ++e) acc[e] += vi[u] * x[u][e];
+            }
+        }
+    }
+    if (fok) store_vec<T, VEC>(Y + ((size_t)b * rows + crow_id[r]) * K + f, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -895,14 +965,45 @@ int launch_long_rows(const int* long_rows, int n_long, const I* indptr, const I*
     return check_launch("rows_long_kernel");
 }
 
+template <typename T, int VEC, int LPR>
+int launch_boo_rows_l(const spmm_boo_desc* A, const T* X, T* Y, int K, int batch, hipStream_t s) {
+    constexpr int RPB = 256 / LPR;
+    const dim3 grid(round_up8((A->n_crow + RPB - 1) / RPB), (K + LPR * VEC - 1) / (LPR * VEC), batch);
+    hipLaunchKernelGGL((boo_rows_kernel<T, VEC, LPR>), grid, dim3(256), 0, s, A->crow_ptr, A->crow_id,
+                       A->ccol, static_cast<const T*>(A->cval), A->n_crow, X, Y, A->rows, A->cols, K);
+    return check_launch("boo_rows_kernel");
+}
+
+template <typename T, int VEC>
+int launch_boo_rows_v(const spmm_boo_desc* A, const T* X, T* Y, int K, int batch, hipStream_t s) {
+    const int need = (K + VEC - 1) / VEC;  // lanes for the whole row
+    if (need <= 1) return launch_boo_rows_l<T, VEC, 1>(A, X, Y, K, batch, s);
+    if (need <= 2) return launch_boo_rows_l<T, VEC, 2>(A, X, Y, K, batch, s);
+    if (need <= 4) return launch_boo_rows_l<T, VEC, 4>(A, X, Y, K, batch, s);
+    if (need <= 8) return launch_boo_rows_l<T, VEC, 8>(A, X, Y, K, batch, s);
+    if (need <= 16) return launch_boo_rows_l<T, VEC, 16>(A, X, Y, K, batch, s);
+    if (need <= 32) return launch_boo_rows_l<T, VEC, 32>(A, X, Y, K, batch, s);
+    return launch_boo_rows_l<T, VEC, 64>(A, X, Y, K, batch, s);
+}
+
+template <typename T>
+int launch_boo_rows(const spmm_boo_desc* A, const T* X, T* Y, int K, int batch, hipStream_t s) {
+    constexpr int V = 16 / sizeof(T);
+    if (K % V == 0 && aligned16(X) && aligned16(Y)) return launch_boo_rows_v<T, V>(A, X, Y, K, batch, s);
+    return launch_boo_rows_v<T, 1>(A, X, Y, K, batch, s);
+}
+
 template <typename T>
 int boo_matmul_t(const spmm_boo_desc* A, const void* Xv, void* Yv, int64_t batch, int64_t K,
                  void* ws, size_t ws_bytes, hipStream_t s) {
     const T* X = static_cast<const T*>(Xv);
     T* Y = static_cast<T*>(Yv);
     if (A->rows == 0 || K == 0 || batch == 0) return SPMM_OK;
-    if (A->n_waves <= 0 || !A->wave_tiles || !A->tiles)
-        return fail(SPMM_EINVAL, "BOO tile stream is empty; stage the matrix with spmm_boo_stage_create");
+    const bool stream = A->n_tiles > 0;
+    if ((!stream && A->n_crow <= 0) || (stream && (A->n_waves <= 0 || !A->wave_tiles || !A->tiles)))
+        return fail(SPMM_EINVAL, "BOO staging is empty; stage the matrix with spmm_boo_stage_create");
+    if (A->n_crow > 0 && (!A->crow_ptr || !A->crow_id))  // ccol/cval may be null when the rows are empty
+        return fail(SPMM_EINVAL, "BOO gather rows are null");
     if (A->cols > 0 && !X) return fail(SPMM_EINVAL, "X is null");
     if (!Y) return fail(SPMM_EINVAL, "Y is null");
     const size_t need = spmm_boo_workspace_bytes(A, sizeof(T) == 4 ? SPMM_F32 : SPMM_F64, batch, K);
@@ -934,8 +1035,12 @@ int boo_matmul_t(const spmm_boo_desc* A, const void* Xv, void* Yv, int64_t batch
     a.X = X;
     a.Y = Y;
     a.P = static_cast<T*>(ws);
-    int rc = boo_dispatch<T>(a, s);
+    int rc = stream ? boo_dispatch<T>(a, s) : SPMM_OK;
     if (rc) return rc;
+    if (A->n_crow > 0) {
+        rc = launch_boo_rows<T>(A, X, Y, (int)K, (int)batch, s);
+        if (rc) return rc;
+    }
     if (A->n_splits > 0) {
         const dim3 grid(A->n_splits, 1, (unsigned)batch);
         hipLaunchKernelGGL((boo_fixup_kernel<T>), grid, dim3(256), 0, s, A->splits, A->row_ids,
@@ -1039,7 +1144,7 @@ struct spmm_boo_stage {
 };
 
 int spmm_boo_stage_create(const spmm_boo_host* H, int32_t max_item_nnz, int32_t long_threshold,
-                          int32_t n_waves, int32_t group, spmm_boo_stage** out) {
+                          int32_t n_waves, int32_t group, float min_reuse, spmm_boo_stage** out) {
     if (!H || !out) return fail(SPMM_EINVAL, "null staging argument");
     *out = nullptr;
     if (H->rows < 0 || H->cols < 0 || H->n_row_groups < 0 || H->n_col_groups < 0 || H->num_blocks < 0)
@@ -1051,6 +1156,7 @@ int spmm_boo_stage_create(const spmm_boo_host* H, int32_t max_item_nnz, int32_t 
     if (max_item_nnz < 1) return fail(SPMM_EINVAL, "max_item_nnz must be positive");
     if (n_waves < 1) return fail(SPMM_EINVAL, "n_waves must be positive");
     if (group != 1 && group != 2 && group != 4) return fail(SPMM_EINVAL, "group must be 1, 2 or 4");
+    if (!(min_reuse >= 0.0f)) return fail(SPMM_EINVAL, "min_reuse must be >= 0");
     if (H->dtype != SPMM_F32 && H->dtype != SPMM_F64) return fail(SPMM_EINVAL, "unknown dtype %d", (int)H->dtype);
     spmm_boo_stage* st = new (std::nothrow) spmm_boo_stage();
     if (!st) return fail(SPMM_ENOMEM, "out of host memory");
@@ -1062,14 +1168,14 @@ int spmm_boo_stage_create(const spmm_boo_host* H, int32_t max_item_nnz, int32_t 
                                               H->blk_row_grp, H->blk_col_grp, H->blk_nz_ptr, H->blk_shift,
                                               H->nz_idx, static_cast<const float*>(H->nz_val), H->rem_indptr,
                                               H->rem_col_ind, static_cast<const float*>(H->rem_vals)};
-            spmm_stage::Builder<float>(in, max_item_nnz, long_threshold, n_waves, group).run(st->s);
+            spmm_stage::Builder<float>(in, max_item_nnz, long_threshold, n_waves, group, min_reuse).run(st->s);
         } else {
             spmm_stage::Builder<double>::In in{H->rows, H->cols, H->n_row_groups, H->n_col_groups, H->num_blocks,
                                                H->row_grp_ptr, H->row_ids, H->col_grp_ptr, H->col_ids,
                                                H->blk_row_grp, H->blk_col_grp, H->blk_nz_ptr, H->blk_shift,
                                                H->nz_idx, static_cast<const double*>(H->nz_val), H->rem_indptr,
                                                H->rem_col_ind, static_cast<const double*>(H->rem_vals)};
-            spmm_stage::Builder<double>(in, max_item_nnz, long_threshold, n_waves, group).run(st->s);
+            spmm_stage::Builder<double>(in, max_item_nnz, long_threshold, n_waves, group, min_reuse).run(st->s);
         }
     } catch (const std::invalid_argument& e) {
         delete st;
@@ -1094,6 +1200,8 @@ int spmm_boo_stage_sizes(const spmm_boo_stage* st, spmm_boo_stage_info* info) {
     info->n_tcols = (int64_t)st->s.tcols.size();
     info->n_splits = (int64_t)(st->s.splits.size() / 4);
     info->n_long = (int64_t)st->s.long_rows.size();
+    info->n_crow = (int64_t)st->s.crow_id.size();
+    info->n_cnz = (int64_t)st->s.ccol.size();
     info->n_slots = st->s.n_slots;
     info->n_waves = st->s.n_waves;
     info->group = st->s.group;
@@ -1102,7 +1210,8 @@ int spmm_boo_stage_sizes(const spmm_boo_stage* st, spmm_boo_stage_info* info) {
 
 int spmm_boo_stage_copy(const spmm_boo_stage* st, int32_t* tiles, uint16_t* tile_rs,
                         void* ent_val, uint8_t* ent_col, int32_t* tcols, int32_t* splits,
-                        int32_t* long_rows, int32_t* wave_tiles) {
+                        int32_t* long_rows, int32_t* wave_tiles, int32_t* crow_ptr, int32_t* crow_id,
+                        int32_t* ccol, void* cval) {
     if (!st) return fail(SPMM_EINVAL, "null staging handle");
     const spmm_stage::Staged& s = st->s;
     auto put = [](void* dst, const void* src, size_t bytes) {
@@ -1116,7 +1225,11 @@ int spmm_boo_stage_copy(const spmm_boo_stage* st, int32_t* tiles, uint16_t* tile
               put(tcols, s.tcols.data(), s.tcols.size() * 4) &&
               put(splits, s.splits.data(), s.splits.size() * 4) &&
               put(long_rows, s.long_rows.data(), s.long_rows.size() * 4) &&
-              put(wave_tiles, s.wave_tiles.data(), s.wave_tiles.size() * 4);
+              put(wave_tiles, s.wave_tiles.data(), s.wave_tiles.size() * 4) &&
+              put(crow_ptr, s.crow_ptr.data(), s.crow_ptr.size() * 4) &&
+              put(crow_id, s.crow_id.data(), s.crow_id.size() * 4) &&
+              put(ccol, s.ccol.data(), s.ccol.size() * 4) &&
+              put(cval, s.cval.data(), s.cval.size());
     return ok ? SPMM_OK : fail(SPMM_EINVAL, "null output array for a non-empty staging field");
 }
 

@@ -55,7 +55,7 @@ def test_version_and_error_path_without_gpu(lib):
 def test_stage_create_rejects_bad_arguments_without_gpu(lib):
     lib.spmm_last_error.restype = ctypes.c_char_p
     out = ctypes.c_void_p(0)
-    rc = lib.spmm_boo_stage_create(None, 4096, 256, 8, 4, ctypes.byref(out))
+    rc = lib.spmm_boo_stage_create(None, 4096, 256, 8, 4, ctypes.c_float(1.5), ctypes.byref(out))
     assert rc == 1 and b'null' in lib.spmm_last_error() and not out.value
     rc = lib.spmm_boo_stage_sizes(None, None)
     assert rc == 1

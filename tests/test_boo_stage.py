@@ -56,6 +56,11 @@ def decode(host, st):
         R.append(host['row_ids'][ro + lr])
         C.append(st['tcols'][co + lc])
         V.append(st['ent_val'][eo:eo + nnz])
+    cp = st['crow_ptr']
+    assert cp[0] == 0 and np.all(np.diff(cp) >= 0) and cp[-1] == len(st['ccol']) == len(st['cval'])
+    R.append(np.repeat(st['crow_id'], np.diff(cp)))
+    C.append(st['ccol'])
+    V.append(st['cval'])
     ip, ci, cv = host['rem_indptr'], host['rem_col_ind'], host['rem_vals']
     for row in st['long_rows']:
         R.append(np.full(ip[row + 1] - ip[row], row))
@@ -64,9 +69,9 @@ def decode(host, st):
     return np.concatenate(R), np.concatenate(C), np.concatenate(V)
 
 
-def check_stream(A, boo, max_item_nnz=4096, long_thr=256, n_waves=64, group=1):
+def check_stream(A, boo, max_item_nnz=4096, long_thr=256, n_waves=64, group=1, min_reuse=0.0):
     host = _host(boo)
-    st = _core.boo_stage(host, max_item_nnz, long_thr, n_waves, group)
+    st = _core.boo_stage(host, max_item_nnz, long_thr, n_waves, group, min_reuse)
     r, c, v = decode(host, st)
     # every stored value exactly once (explicit zeros included)
     got = sp.coo_matrix((np.ones_like(v, dtype=np.int64), (r, c)), shape=A.shape).tocsr()
@@ -77,8 +82,17 @@ def check_stream(A, boo, max_item_nnz=4096, long_thr=256, n_waves=64, group=1):
     # items / waves
     tiles = st['tiles'].reshape(-1, 8)
     last = (tiles[:, 1] >> 24) & 1
-    assert last[-1] == 1
+    # every Y row is stored exactly once: by the last tile of its slice's
+    # first item, or by the gather pass
+    owner = tiles[(last == 1) & (tiles[:, 4] == -1)]
+    stored = [host['row_ids'][ro:ro + ((w1 >> 16) & 0xff)] for _, w1, _, ro, *_ in owner]
+    stored = np.concatenate(stored + [st['crow_id']])
+    assert np.array_equal(np.sort(stored), np.arange(A.shape[0]))
     wt = st['wave_tiles']
+    if len(tiles) == 0:
+        assert st['n_waves'] == 0 and list(wt) == [0]
+        return st
+    assert last[-1] == 1
     assert wt[0] == 0 and wt[-1] == len(tiles) and np.all(np.diff(wt) > 0)
     assert st['n_waves'] == len(wt) - 1 <= max(n_waves, group) and st['n_waves'] % group == 0
     for w in range(1, len(wt) - 1):
@@ -105,11 +119,15 @@ def check_stream(A, boo, max_item_nnz=4096, long_thr=256, n_waves=64, group=1):
 @pytest.mark.parametrize('policy', ['keep', 'remainder', 'tail_batch'])
 @pytest.mark.parametrize('order', ['rowmajor', 'colmajor'])
 @pytest.mark.parametrize('group', [1, 2, 4])
-def test_stream_covers_every_entry(policy, order, group):
-    A = sp.random(300, 260, density=0.05, format='csr', random_state=7, dtype=np.float32)
+@pytest.mark.parametrize('min_reuse', [0.0, 1.5])
+def test_stream_covers_every_entry(policy, order, group, min_reuse):
+    A = sp.random(300, 260, density=0.05, format='lil', random_state=7, dtype=np.float32)
+    A[:40] = 0.0                        # a few empty slices
+    A = A.tocsr()
+    A.eliminate_zeros()
     boo = S.csr_to_boo(A, cluster='random', target_nr=16, target_nc=24, small_block_policy=policy,
                        nz_order=order, seed=3)
-    check_stream(A, boo, group=group)
+    check_stream(A, boo, group=group, min_reuse=min_reuse)
 
 
 @pytest.mark.parametrize('nr,nc', [(32, 32), (64, 64), (8, 100), (100, 8)])
@@ -147,6 +165,26 @@ def test_stream_empty_rows_get_a_tile():
     st = _core.boo_stage(host, 4096, 256, 8, 1)
     tiles = st['tiles'].reshape(-1, 8)
     assert len(tiles) == 3 and np.all(tiles[:, 1] & 0xff == 0)   # 70 rows -> 3 slices
+    assert len(st['crow_id']) == 0
+
+
+def test_gather_pass_takes_empty_and_scattered_slices():
+    # empty slices: rows with no entries, stored as zeros by the gather pass
+    A = sp.csr_matrix((70, 50), dtype=np.float32)
+    boo = S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32)
+    st = check_stream(A, boo, min_reuse=1.5)
+    assert len(st['tiles']) == 0 and sorted(st['crow_id']) == list(range(70))
+    assert np.all(np.diff(st['crow_ptr']) == 0)
+    # a permuted stencil: every slice's columns are scattered (each used ~once)
+    Ap = M.permuted(M.stencil_27pt(16), seed=1)
+    boo = S.csr_to_boo(Ap, cluster='identity', target_nr=32, target_nc=32)
+    st = check_stream(Ap, boo, min_reuse=1.5, group=4)
+    assert len(st['crow_id']) > 0.9 * Ap.shape[0]
+    # the same matrix unpermuted keeps its slices in the tile stream
+    As = M.stencil_27pt(8)
+    boo = S.csr_to_boo(As, cluster='identity', target_nr=32, target_nc=32)
+    st = check_stream(As, boo, min_reuse=1.5, group=4)
+    assert len(st['crow_id']) == 0
 
 
 def test_stream_config2_counts():
@@ -162,7 +200,8 @@ def test_stream_config2_counts():
     assert 2000 <= st['n_waves'] <= 2048 and st['n_slots'] == 0
     # grouped by 4: the 27-point stencil's row groups share column groups, so
     # a group of 4 loads far fewer X tiles than 4 separate row groups
-    st4 = _core.boo_stage(host, 4096, 256, 4096, 4)
+    st4 = _core.boo_stage(host, 4096, 256, 4096, 4, 1.5)
+    assert len(st4['crow_id']) == 0         # reuse ~2.9 per column: all slices stay tiles
     t4 = st4['tiles'].reshape(-1, 8)
     assert (t4[:, 1] & 0xff).sum() == A.nnz
     steps = len(t4) // 4

@@ -21,6 +21,14 @@ POLICIES = ['keep', 'remainder', 'tail_batch']
 ORDERS = ['rowmajor', 'colmajor']
 
 
+@pytest.fixture(autouse=True, params=['tile', 'gather'])
+def path(request, monkeypatch):
+    """Run every case twice: with every slice in the tile stream, and with
+    every slice light enough sent to the row-wise gather pass."""
+    monkeypatch.setattr(SB, 'MIN_COL_REUSE', 0.0 if request.param == 'tile' else 1e9)
+    return request.param
+
+
 def _tol(dtype):
     return 1e-5 if dtype in (torch.float32, np.float32) else 1e-12
 
@@ -318,3 +326,35 @@ def test_benchmark_configs_full_size(cfg):
     lin = S.boo_matmul(boo, x + x2) - y - S.boo_matmul(boo, x2)
     bound = torch.from_numpy(abs(A) @ (np.abs(x.cpu().numpy()) + np.abs(x2.cpu().numpy()))).cuda()
     assert torch.all(lin.abs() <= 3e-5 * bound)
+
+
+@pytest.mark.parametrize('K', [1, 5, 32, 64, 128, 256, 300])
+@pytest.mark.parametrize('dtype', [torch.float32, torch.float64])
+def test_scattered_columns_take_the_gather_pass(K, dtype, monkeypatch):
+    from spmm_amd import matrices as M
+    monkeypatch.setattr(SB, 'MIN_COL_REUSE', 1.5)      # the default
+    np_dtype = np.float32 if dtype == torch.float32 else np.float64
+    A = M.permuted(M.stencil_27pt(16, dtype=np_dtype), seed=1)
+    boo = S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32).to('cuda')
+    assert boo._gpu_meta.desc['n_crow'] > 0.9 * A.shape[0]
+    x = _x((2, A.shape[1], K), dtype).cuda()
+    check(S.boo_matmul(boo, x), A, x)
+
+
+@pytest.mark.parametrize('which', ['rmat', 'permuted_stencil'])
+def test_scaled_down_power_law_and_permuted_configs(which, monkeypatch):
+    """Configs 4 and 5 at reduced size: heavy slices split into items, long
+    remainder rows, scattered slices in the gather pass, all at once."""
+    from spmm_amd import matrices as M
+    monkeypatch.setattr(SB, 'MIN_COL_REUSE', 1.5)
+    if which == 'rmat':
+        A, K = M.rmat(14, 16), 128
+    else:
+        A, K = M.permuted(M.stencil_27pt(32)), 32
+    boo = S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32).to('cuda')
+    d = boo._gpu_meta.desc
+    assert d['n_crow'] > 0
+    x = torch.from_numpy(M.dense_x(A.shape[1], K)).cuda()
+    y = S.boo_matmul(boo, x)
+    check(y, A, x)
+    assert torch.equal(S.boo_matmul(boo, x), y)
