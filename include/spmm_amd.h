@@ -109,8 +109,8 @@ typedef struct spmm_boo_host {
 typedef struct spmm_boo_stage spmm_boo_stage;  /* opaque, host memory */
 
 typedef struct spmm_boo_stage_info {
-    int64_t n_tiles, n_ent, n_tcols, n_splits, n_long, n_crow, n_cnz;
-    int32_t n_slots, n_waves, group;
+    int64_t n_tiles, n_ent, n_tcols, n_splits, n_long, n_crow, n_cnz, n_gtask;
+    int32_t n_slots, n_waves, group, n_crow_long;
 } spmm_boo_stage_info;
 
 /* group (1, 2 or 4): slices that share column chunks are put together, up to
@@ -130,13 +130,17 @@ int spmm_boo_stage_sizes(const spmm_boo_stage* st, spmm_boo_stage_info* info);
  *   tcols [n_tcols] int32, splits [n_splits*4] int32, long_rows [n_long] int32,
  *   wave_tiles [n_waves+1] int32,
  *   crow_ptr [n_crow+1] int32, crow_id [n_crow] int32, ccol [n_cnz] int32, cval [n_cnz] (dtype):
- *   the rows of the gather pass (Y row ids, their entries with global columns).
+ *   the rows of the gather pass (Y row ids, their entries with global columns);
+ *   the last n_crow_long of them are longer than long_threshold and are summed in
+ *   chunk tasks: gtask [n_gtask*2] int32 (entry begin, end), gtask_ptr [n_crow_long+1]
+ *   int32 (long row i owns tasks gtask_ptr[i] .. gtask_ptr[i+1]).
  * Every tile's entries start at an even index (odd tiles are followed by a
  * zero entry). */
 int spmm_boo_stage_copy(const spmm_boo_stage* st, int32_t* tiles, uint16_t* tile_rs,
                         void* ent_val, uint8_t* ent_col, int32_t* tcols, int32_t* splits,
                         int32_t* long_rows, int32_t* wave_tiles, int32_t* crow_ptr,
-                        int32_t* crow_id, int32_t* ccol, void* cval);
+                        int32_t* crow_id, int32_t* ccol, void* cval, int32_t* gtask,
+                        int32_t* gtask_ptr);
 void spmm_boo_stage_destroy(spmm_boo_stage* st);
 
 /* Device descriptor: the staged arrays plus row_ids and the remainder CSR
@@ -163,12 +167,17 @@ typedef struct spmm_boo_desc {
     const int32_t* crow_id;      /* [n_crow] */
     const int32_t* ccol;         /* [n_cnz] (may be null when n_cnz is 0) */
     const void* cval;            /* [n_cnz] (may be null when n_cnz is 0) */
+    int32_t n_crow_long;         /* the last n_crow_long gather rows are summed in chunk tasks */
+    int32_t n_gtask;
+    const int32_t* gtask;        /* [n_gtask*2] */
+    const int32_t* gtask_ptr;    /* [n_crow_long+1] */
     const int32_t* rem_indptr;   /* [rows+1] */
     const int32_t* rem_col_ind;
     const void* rem_vals;
 } spmm_boo_desc;
 
-/* Workspace bytes spmm_boo_matmul needs for this staging and shape. */
+/* Workspace bytes spmm_boo_matmul needs for this staging and shape: the
+ * partial slots of split slices and the partial rows of chunk tasks. */
 size_t spmm_boo_workspace_bytes(const spmm_boo_desc* A, spmm_dtype dtype, int64_t batch, int64_t K);
 
 /* Y[b] = A X[b] for b < batch.  X: [batch][A->cols][K], Y: [batch][A->rows][K].

@@ -242,7 +242,7 @@ def _boo_to(self, device='cuda'):
     # the remainder CSR with the tail folded in, read by the long-row pass.
     meta.stage = types.SimpleNamespace(**{k: _pinned(stage[k], device) for k in (
         'tiles', 'tile_rs', 'ent_val', 'ent_col', 'tcols', 'splits', 'long_rows',
-        'wave_tiles', 'crow_ptr', 'crow_id', 'ccol', 'cval')})
+        'wave_tiles', 'crow_ptr', 'crow_id', 'ccol', 'cval', 'gtask', 'gtask_ptr')})
     if self.tail_nnz():
         meta.k_rem_indptr = _pinned(k_rem_indptr, device)
         meta.k_rem_col_ind = _pinned(k_rem_col, device)
@@ -263,7 +263,8 @@ def _boo_to(self, device='cuda'):
         'n_slots': int(stage['n_slots']), 'n_splits': int(stage['n_splits']), 'splits': p(g.splits),
         'n_long': int(stage['n_long']), 'long_rows': p(g.long_rows),
         'n_crow': int(stage['n_crow']), 'crow_ptr': p(g.crow_ptr), 'crow_id': p(g.crow_id),
-        'ccol': p(g.ccol), 'cval': p(g.cval),
+        'ccol': p(g.ccol), 'cval': p(g.cval), 'n_crow_long': int(stage['n_crow_long']),
+        'n_gtask': int(stage['n_gtask']), 'gtask': p(g.gtask), 'gtask_ptr': p(g.gtask_ptr),
         'rem_indptr': p(meta.k_rem_indptr), 'rem_col_ind': p(meta.k_rem_col_ind),
         'rem_vals': p(meta.k_rem_vals),
     }

@@ -57,6 +57,11 @@ constexpr int SERIAL_MAX_BUSY = 8;    // busy rows a serial tile may have
 constexpr long long COST_STEP = 256;
 constexpr long long COST_ITEM = 512;
 
+// Gather-pass rows longer than the long-row threshold are summed in chunks of
+// at most GATHER_CHUNK entries, one workgroup each, into partial rows that a
+// fixup pass adds in chunk order.
+constexpr int GATHER_CHUNK = 1024;
+
 
 
 struct Staged {
@@ -75,6 +80,11 @@ struct Staged {
     std::vector<int32_t> crow_id;    // [n_crow]
     std::vector<int32_t> ccol;       // [n_cnz]
     std::vector<char> cval;          // [n_cnz] values (float or double bytes)
+    // the last n_crow_long gather rows are long: chunk tasks (entry begin,
+    // end) of long row i are gtask[gtask_ptr[i] .. gtask_ptr[i+1])
+    int32_t n_crow_long = 0;
+    std::vector<int32_t> gtask;      // [n_gtask][2]
+    std::vector<int32_t> gtask_ptr;  // [n_crow_long+1]
     int32_t n_slots = 0;
     int32_t n_waves = 0;
     int32_t group = 1;               // waves per workgroup sharing X tiles
@@ -104,11 +114,10 @@ public:
         const T* rem_vals;
     };
 
-    // min_reuse: a slice whose nonzeros use each of their distinct columns
-    // fewer than min_reuse times on average (scattered columns: a permuted or
-    // power-law matrix) gains nothing from staging X tiles, and its rows go to
-    // the row-wise gather pass, as do empty slices; 0 keeps every slice in
-    // the tile stream.
+    // min_reuse: a slice with fewer than min_reuse nonzeros per X row its
+    // tiles would stage (scattered columns: a permuted or power-law matrix)
+    // gains nothing from staging X tiles, and its rows go to the row-wise
+    // gather pass, as do empty slices; 0 keeps every slice in the tile stream.
     Builder(const In& in, int max_item_nnz, int long_threshold, int n_waves, int group, float min_reuse)
         : in_(in), max_item_nnz_(max_item_nnz), long_threshold_(long_threshold),
           want_waves_(n_waves), G_(group), min_reuse_(min_reuse) {}
@@ -119,6 +128,9 @@ public:
         S.tcols.assign(in_.col_ids, in_.col_ids + in_.cols);
         collect_slices(S);
         classify_slices();
+        for (const Slice& sl : slices_)  // long remainder rows of the tile stream's slices
+            if (!sl.csr)
+                for (size_t i = sl.g0; i < sl.g1; ++i) S.long_rows.push_back(longs_[i].row);
         make_groups();
         for (size_t g = 0; g < groups_.size(); ++g) build_group_steps(S, g);
         split_heavy(S);
@@ -136,8 +148,12 @@ private:
         int row_off, nr;
         size_t c0, c1;  // chunks in chunks_
         size_t r0, r1;  // remainder entries in pool_ (lc = 0; column in rcol_)
+        size_t g0, g1;  // its long remainder rows in longs_
         long long nnz;
         bool csr;       // rows go to the gather pass, not the tile stream
+    };
+    struct LongRow {
+        int32_t lr, row;
     };
     // ---- one step of a group: one X tile, each member's entries in it
     struct Step {
@@ -215,13 +231,14 @@ private:
                 }
                 sl.c1 = chunks_.size();
                 sl.r0 = pool_.size();
+                sl.g0 = longs_.size();
                 for (int lr = 0; lr < sl.nr; ++lr) {
                     const int row = in_.row_ids[sl.row_off + lr];
                     if (row < 0 || row >= in_.rows) throw std::invalid_argument("row_ids out of range");
                     const int rs = in_.rem_indptr[row], re = in_.rem_indptr[row + 1];
                     if (re == rs) continue;
                     if (re - rs > long_threshold_) {
-                        S.long_rows.push_back(row);
+                        longs_.push_back(LongRow{lr, row});
                         continue;
                     }
                     for (int j = rs; j < re; ++j) {
@@ -232,6 +249,7 @@ private:
                     sl.nnz += re - rs;
                 }
                 sl.r1 = pool_.size();
+                sl.g1 = longs_.size();
                 slices_.push_back(sl);
             }
         }
@@ -244,30 +262,31 @@ private:
         return c ? in_.col_ids[c->cid_off + pool_[e].lc] : rcol_[e];
     }
 
-    // Send empty slices and slices with scattered columns to the gather pass.
-    // A slice heavier than max_item_nnz stays in the stream, where it is cut
-    // into items that run in parallel.
+    // Send empty slices, and slices whose tiles would stage more X rows than
+    // min_reuse per entry allows, to the gather pass.  A slice's tiles stage
+    // every column of each block chunk it touches plus its remainder's
+    // distinct columns.
     void classify_slices() {
-        std::vector<int32_t> cols;
         if (!(min_reuse_ > 0.0f)) return;
+        std::vector<int32_t> cols;
         for (Slice& sl : slices_) {
             if (sl.nnz == 0) {
                 sl.csr = true;
                 continue;
             }
-            if (sl.nnz > max_item_nnz_) continue;
-            cols.clear();
-            for (size_t c = sl.c0; c < sl.c1; ++c)
-                for (size_t e = chunks_[c].e0; e < chunks_[c].e1; ++e) cols.push_back(ent_col_of(e, &chunks_[c]));
-            for (size_t e = sl.r0; e < sl.r1; ++e) cols.push_back(rcol_[e]);
+            long long staged = 0;
+            for (size_t c = sl.c0; c < sl.c1; ++c) staged += chunks_[c].nc;
+            cols.assign(rcol_.begin() + sl.r0, rcol_.begin() + sl.r1);
             std::sort(cols.begin(), cols.end());
-            const long long distinct = std::unique(cols.begin(), cols.end()) - cols.begin();
-            sl.csr = (double)sl.nnz < (double)min_reuse_ * (double)distinct;
+            staged += std::unique(cols.begin(), cols.end()) - cols.begin();
+            sl.csr = (double)sl.nnz < (double)min_reuse_ * (double)staged;
         }
     }
 
-    // The gather pass's rows: every row of every slice sent there, with its
-    // block entries (in block order) and then its short remainder entries.
+    // The gather pass's rows: every row of every slice sent there, whole (its
+    // block entries in block order, then its remainder, long or not).  Rows of
+    // at most long_threshold entries come first, in slice order; the longer
+    // ones follow, each cut into chunk tasks.
     void emit_csr(Staged& S) {
         struct RE {
             int32_t lr, col;
@@ -275,7 +294,14 @@ private:
             int32_t from_rem;
         };
         std::vector<RE> v;
+        std::vector<int32_t> long_id, long_ptr(1, 0), long_col;
+        std::vector<T> long_val;
         S.crow_ptr.assign(1, 0);
+        auto put = [](std::vector<int32_t>& cols, std::vector<char>& vals, int32_t col, T x) {
+            cols.push_back(col);
+            const char* p = reinterpret_cast<const char*>(&x);
+            vals.insert(vals.end(), p, p + sizeof(T));
+        };
         for (const Slice& sl : slices_) {
             if (!sl.csr) continue;
             v.clear();
@@ -283,19 +309,49 @@ private:
                 for (size_t e = chunks_[c].e0; e < chunks_[c].e1; ++e)
                     v.push_back(RE{pool_[e].lr, ent_col_of(e, &chunks_[c]), pool_[e].src, 0});
             for (size_t e = sl.r0; e < sl.r1; ++e) v.push_back(RE{pool_[e].lr, rcol_[e], pool_[e].src, 1});
+            for (size_t i = sl.g0; i < sl.g1; ++i) {
+                const int row = longs_[i].row;
+                for (int j = in_.rem_indptr[row]; j < in_.rem_indptr[row + 1]; ++j)
+                    v.push_back(RE{longs_[i].lr, in_.rem_col_ind[j], j, 1});
+            }
             std::stable_sort(v.begin(), v.end(), [](const RE& a, const RE& b) { return a.lr < b.lr; });
             size_t k = 0;
             for (int lr = 0; lr < sl.nr; ++lr) {
-                S.crow_id.push_back(in_.row_ids[sl.row_off + lr]);
-                for (; k < v.size() && v[k].lr == lr; ++k) {
-                    S.ccol.push_back(v[k].col);
+                size_t k1 = k;
+                while (k1 < v.size() && v[k1].lr == lr) ++k1;
+                const int32_t row = in_.row_ids[sl.row_off + lr];
+                const bool is_long = (long long)(k1 - k) > (long long)long_threshold_;
+                for (; k < k1; ++k) {
                     const T x = v[k].from_rem ? in_.rem_vals[v[k].src] : in_.nz_val[v[k].src];
-                    const char* p = reinterpret_cast<const char*>(&x);
-                    S.cval.insert(S.cval.end(), p, p + sizeof(T));
+                    if (is_long) {
+                        long_col.push_back(v[k].col);
+                        long_val.push_back(x);
+                    } else {
+                        put(S.ccol, S.cval, v[k].col, x);
+                    }
                 }
-                S.crow_ptr.push_back((int32_t)S.ccol.size());
+                if (is_long) {
+                    long_id.push_back(row);
+                    long_ptr.push_back((int32_t)long_col.size());
+                } else {
+                    S.crow_id.push_back(row);
+                    S.crow_ptr.push_back((int32_t)S.ccol.size());
+                }
             }
         }
+        S.n_crow_long = (int32_t)long_id.size();
+        S.gtask_ptr.assign(1, 0);
+        const int32_t base = (int32_t)S.ccol.size();
+        for (size_t i = 0; i < long_id.size(); ++i) {
+            S.crow_id.push_back(long_id[i]);
+            for (int32_t e = long_ptr[i]; e < long_ptr[i + 1]; e += GATHER_CHUNK) {
+                S.gtask.push_back(base + e);
+                S.gtask.push_back(base + std::min(long_ptr[i + 1], e + GATHER_CHUNK));
+            }
+            S.gtask_ptr.push_back((int32_t)(S.gtask.size() / 2));
+            S.crow_ptr.push_back(base + long_ptr[i + 1]);
+        }
+        for (size_t e = 0; e < long_col.size(); ++e) put(S.ccol, S.cval, long_col[e], long_val[e]);
     }
 
     // Slices that share column chunks go into one group (up to G): a group
@@ -626,6 +682,7 @@ private:
     std::vector<Ent> pool_, tent_;
     std::vector<int32_t> rcol_, colx_;
     std::vector<Chunk> chunks_;
+    std::vector<LongRow> longs_;
     std::vector<Slice> slices_;
     std::vector<Group> groups_;
     std::vector<Step> steps_;

@@ -291,6 +291,10 @@ spmm_boo_desc boo_desc(const py::dict& d) {
     A.crow_id = reinterpret_cast<const int32_t*>(P(d, "crow_id"));
     A.ccol = reinterpret_cast<const int32_t*>(P(d, "ccol"));
     A.cval = reinterpret_cast<const void*>(P(d, "cval"));
+    A.n_crow_long = d["n_crow_long"].cast<int32_t>();
+    A.n_gtask = d["n_gtask"].cast<int32_t>();
+    A.gtask = reinterpret_cast<const int32_t*>(P(d, "gtask"));
+    A.gtask_ptr = reinterpret_cast<const int32_t*>(P(d, "gtask_ptr"));
     A.rem_indptr = reinterpret_cast<const int32_t*>(P(d, "rem_indptr"));
     A.rem_col_ind = reinterpret_cast<const int32_t*>(P(d, "rem_col_ind"));
     A.rem_vals = reinterpret_cast<const void*>(P(d, "rem_vals"));
@@ -333,7 +337,8 @@ py::dict boo_stage(const py::dict& h, int32_t max_item_nnz, int32_t long_thresho
     spmm_boo_stage_sizes(st, &inf);
     std::vector<int32_t> tiles((size_t)inf.n_tiles * 8), tcols((size_t)inf.n_tcols),
         splits((size_t)inf.n_splits * 4), longr((size_t)inf.n_long), wt((size_t)inf.n_waves + 1),
-        crp((size_t)inf.n_crow + 1), cri((size_t)inf.n_crow), ccol((size_t)inf.n_cnz);
+        crp((size_t)inf.n_crow + 1), cri((size_t)inf.n_crow), ccol((size_t)inf.n_cnz),
+        gt((size_t)inf.n_gtask * 2), gtp((size_t)inf.n_crow_long + 1);
     std::vector<uint16_t> rs((size_t)inf.n_tiles * 33);
     std::vector<uint8_t> ecol((size_t)inf.n_ent);
     py::array ev = f64 ? py::array(py::array_t<double>((py::ssize_t)inf.n_ent))
@@ -343,7 +348,7 @@ py::dict boo_stage(const py::dict& h, int32_t max_item_nnz, int32_t long_thresho
     const int rc = spmm_boo_stage_copy(st, tiles.data(), rs.data(), inf.n_ent ? ev.mutable_data() : nullptr,
                                        ecol.data(), tcols.data(), splits.data(), longr.data(), wt.data(),
                                        crp.data(), cri.data(), ccol.data(),
-                                       inf.n_cnz ? cv.mutable_data() : nullptr);
+                                       inf.n_cnz ? cv.mutable_data() : nullptr, gt.data(), gtp.data());
     spmm_boo_stage_destroy(st);
     raise_status(rc);
     py::dict d;
@@ -360,6 +365,10 @@ py::dict boo_stage(const py::dict& h, int32_t max_item_nnz, int32_t long_thresho
     d["ccol"] = give(std::move(ccol));
     d["cval"] = cv;
     d["n_crow"] = inf.n_crow;
+    d["gtask"] = give(std::move(gt));
+    d["gtask_ptr"] = give(std::move(gtp));
+    d["n_crow_long"] = inf.n_crow_long;
+    d["n_gtask"] = inf.n_gtask;
     d["n_tiles"] = inf.n_tiles;
     d["n_slots"] = inf.n_slots;
     d["n_splits"] = inf.n_splits;

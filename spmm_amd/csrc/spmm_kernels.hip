@@ -649,6 +649,86 @@ __global__ void __launch_bounds__(256) boo_rows_kernel(const int* __restrict__ c
     if (fok) store_vec<T, VEC>(Y + ((size_t)b * rows + crow_id[r]) * K + f, acc);
 }
 
+// Long gather rows: one workgroup per chunk task (at most a fixed number of
+// one row's entries), 16 entry slots x 16 lanes of VEC features, U entries per
+// slot in flight; the slots' sums are reduced in a fixed order through LDS
+// into the task's partial row P[task][b][:].
+template <typename T, int VEC>
+__global__ void __launch_bounds__(256) gather_chunk_kernel(const int* __restrict__ gtask,
+                                                           const int* __restrict__ ccol,
+                                                           const T* __restrict__ cval,
+                                                           const T* __restrict__ X, T* __restrict__ P,
+                                                           int cols, int K, int batch) {
+    constexpr int LANES = 16, SLOTS = 16, KT = LANES * VEC, U = 4;
+    __shared__ T red[SLOTS][KT];
+    const int t = blockIdx.x;
+    const int b = blockIdx.z;
+    const int slot = threadIdx.x / LANES;
+    const int ch = threadIdx.x % LANES;
+    const int f = (int)blockIdx.y * KT + ch * VEC;
+    const bool fok = f < K;  // K is a multiple of VEC
+    const T* Xb = X + (size_t)b * cols * K;
+    T acc[VEC];
+#pragma unroll
+    for (int u = 0; u < VEC; ++u) acc[u] = T(0);
+    const int e0 = gtask[2 * t], e1 = gtask[2 * t + 1];
+    if (fok) {
+        int j = e0 + slot;
+        for (; j + (U - 1) * SLOTS < e1; j += U * SLOTS) {
+            int c[U];
+            T v[U], x[U][VEC];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                c[u] = ccol[j + u * SLOTS];
+                v[u] = cval[j + u * SLOTS];
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) load_vec<T, VEC>(Xb + (size_t)c[u] * K + f, x[u]);
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) acc[e] += v[u] * x[u][e];
+        }
+        for (; j < e1; j += SLOTS) {
+            T x[VEC];
+            load_vec<T, VEC>(Xb + (size_t)ccol[j] * K + f, x);
+            const T v = cval[j];
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) acc[e] += v * x[e];
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < VEC; ++u) red[slot][ch * VEC + u] = acc[u];
+    __syncthreads();
+    if (threadIdx.x < KT) {
+        const int fe = (int)blockIdx.y * KT + (int)threadIdx.x;
+        if (fe < K) {
+            T sum = T(0);
+#pragma unroll
+            for (int sl = 0; sl < SLOTS; ++sl) sum += red[sl][threadIdx.x];
+            P[((size_t)t * batch + b) * K + fe] = sum;
+        }
+    }
+}
+
+// Long gather row i: Y[crow_id[r0 + i]] = sum of its tasks' partial rows, in
+// task order (deterministic).
+template <typename T>
+__global__ void __launch_bounds__(256) gather_fix_kernel(const int* __restrict__ gtask_ptr,
+                                                         const int* __restrict__ crow_id, int r0,
+                                                         const T* __restrict__ P, T* __restrict__ Y,
+                                                         int rows, int K, int batch) {
+    const int i = blockIdx.x;
+    const int b = blockIdx.z;
+    const int yrow = crow_id[r0 + i];
+    const int t0 = gtask_ptr[i], t1 = gtask_ptr[i + 1];
+    for (int f = threadIdx.x; f < K; f += blockDim.x) {
+        T sum = T(0);
+        for (int t = t0; t < t1; ++t) sum += P[((size_t)t * batch + b) * K + f];
+        Y[((size_t)b * rows + yrow) * K + f] = sum;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Long remainder rows (BOO and PBR): Y[row] += sum over the row's CSR entries.
 // 256 threads = 16 nonzero slots x 16 lanes of VEC features.
@@ -965,12 +1045,21 @@ int launch_long_rows(const int* long_rows, int n_long, const I* indptr, const I*
     return check_launch("rows_long_kernel");
 }
 
+// Workspace: the partial slots of split slices, then (256-byte aligned) the
+// partial rows of the long gather rows' chunk tasks.
+inline size_t boo_ws_slots_bytes(const spmm_boo_desc* A, size_t es, int64_t batch, int64_t K) {
+    const size_t slots = A->n_slots > 0 ? (size_t)A->n_slots * (size_t)batch * (size_t)ST_ROWS * (size_t)K * es : 0;
+    return (slots + 255) / 256 * 256;
+}
+
 template <typename T, int VEC, int LPR>
 int launch_boo_rows_l(const spmm_boo_desc* A, const T* X, T* Y, int K, int batch, hipStream_t s) {
     constexpr int RPB = 256 / LPR;
-    const dim3 grid(round_up8((A->n_crow + RPB - 1) / RPB), (K + LPR * VEC - 1) / (LPR * VEC), batch);
+    const int n_short = A->n_crow - A->n_crow_long;
+    if (n_short <= 0) return SPMM_OK;
+    const dim3 grid(round_up8((n_short + RPB - 1) / RPB), (K + LPR * VEC - 1) / (LPR * VEC), batch);
     hipLaunchKernelGGL((boo_rows_kernel<T, VEC, LPR>), grid, dim3(256), 0, s, A->crow_ptr, A->crow_id,
-                       A->ccol, static_cast<const T*>(A->cval), A->n_crow, X, Y, A->rows, A->cols, K);
+                       A->ccol, static_cast<const T*>(A->cval), n_short, X, Y, A->rows, A->cols, K);
     return check_launch("boo_rows_kernel");
 }
 
@@ -987,10 +1076,26 @@ int launch_boo_rows_v(const spmm_boo_desc* A, const T* X, T* Y, int K, int batch
 }
 
 template <typename T>
-int launch_boo_rows(const spmm_boo_desc* A, const T* X, T* Y, int K, int batch, hipStream_t s) {
+int launch_boo_rows(const spmm_boo_desc* A, const T* X, T* Y, int K, int batch, T* P2, hipStream_t s) {
     constexpr int V = 16 / sizeof(T);
-    if (K % V == 0 && aligned16(X) && aligned16(Y)) return launch_boo_rows_v<T, V>(A, X, Y, K, batch, s);
-    return launch_boo_rows_v<T, 1>(A, X, Y, K, batch, s);
+    const bool vec = K % V == 0 && aligned16(X) && aligned16(Y);
+    int rc = vec ? launch_boo_rows_v<T, V>(A, X, Y, K, batch, s) : launch_boo_rows_v<T, 1>(A, X, Y, K, batch, s);
+    if (rc || A->n_crow_long <= 0) return rc;
+    if (A->n_gtask > 0) {
+        const int v = vec ? V : 1;
+        const dim3 grid(A->n_gtask, (K + 16 * v - 1) / (16 * v), batch);
+        if (vec)
+            hipLaunchKernelGGL((gather_chunk_kernel<T, V>), grid, dim3(256), 0, s, A->gtask, A->ccol,
+                               static_cast<const T*>(A->cval), X, P2, A->cols, K, batch);
+        else
+            hipLaunchKernelGGL((gather_chunk_kernel<T, 1>), grid, dim3(256), 0, s, A->gtask, A->ccol,
+                               static_cast<const T*>(A->cval), X, P2, A->cols, K, batch);
+        rc = check_launch("gather_chunk_kernel");
+        if (rc) return rc;
+    }
+    hipLaunchKernelGGL((gather_fix_kernel<T>), dim3(A->n_crow_long, 1, batch), dim3(256), 0, s, A->gtask_ptr,
+                       A->crow_id, A->n_crow - A->n_crow_long, (const T*)P2, Y, A->rows, K, batch);
+    return check_launch("gather_fix_kernel");
 }
 
 template <typename T>
@@ -1004,6 +1109,9 @@ int boo_matmul_t(const spmm_boo_desc* A, const void* Xv, void* Yv, int64_t batch
         return fail(SPMM_EINVAL, "BOO staging is empty; stage the matrix with spmm_boo_stage_create");
     if (A->n_crow > 0 && (!A->crow_ptr || !A->crow_id))  // ccol/cval may be null when the rows are empty
         return fail(SPMM_EINVAL, "BOO gather rows are null");
+    if (A->n_crow_long < 0 || A->n_crow_long > A->n_crow || A->n_gtask < 0 ||
+        (A->n_crow_long > 0 && !A->gtask_ptr) || (A->n_gtask > 0 && !A->gtask))
+        return fail(SPMM_EINVAL, "bad BOO long gather rows");
     if (A->cols > 0 && !X) return fail(SPMM_EINVAL, "X is null");
     if (!Y) return fail(SPMM_EINVAL, "Y is null");
     const size_t need = spmm_boo_workspace_bytes(A, sizeof(T) == 4 ? SPMM_F32 : SPMM_F64, batch, K);
@@ -1038,7 +1146,11 @@ int boo_matmul_t(const spmm_boo_desc* A, const void* Xv, void* Yv, int64_t batch
     int rc = stream ? boo_dispatch<T>(a, s) : SPMM_OK;
     if (rc) return rc;
     if (A->n_crow > 0) {
-        rc = launch_boo_rows<T>(A, X, Y, (int)K, (int)batch, s);
+        rc = launch_boo_rows<T>(A, X, Y, (int)K, (int)batch,
+                                ws ? reinterpret_cast<T*>(static_cast<char*>(ws) +
+                                                          boo_ws_slots_bytes(A, sizeof(T), batch, K))
+                                   : nullptr,
+                                s);
         if (rc) return rc;
     }
     if (A->n_splits > 0) {
@@ -1202,6 +1314,8 @@ int spmm_boo_stage_sizes(const spmm_boo_stage* st, spmm_boo_stage_info* info) {
     info->n_long = (int64_t)st->s.long_rows.size();
     info->n_crow = (int64_t)st->s.crow_id.size();
     info->n_cnz = (int64_t)st->s.ccol.size();
+    info->n_crow_long = st->s.n_crow_long;
+    info->n_gtask = (int64_t)(st->s.gtask.size() / 2);
     info->n_slots = st->s.n_slots;
     info->n_waves = st->s.n_waves;
     info->group = st->s.group;
@@ -1211,7 +1325,7 @@ int spmm_boo_stage_sizes(const spmm_boo_stage* st, spmm_boo_stage_info* info) {
 int spmm_boo_stage_copy(const spmm_boo_stage* st, int32_t* tiles, uint16_t* tile_rs,
                         void* ent_val, uint8_t* ent_col, int32_t* tcols, int32_t* splits,
                         int32_t* long_rows, int32_t* wave_tiles, int32_t* crow_ptr, int32_t* crow_id,
-                        int32_t* ccol, void* cval) {
+                        int32_t* ccol, void* cval, int32_t* gtask, int32_t* gtask_ptr) {
     if (!st) return fail(SPMM_EINVAL, "null staging handle");
     const spmm_stage::Staged& s = st->s;
     auto put = [](void* dst, const void* src, size_t bytes) {
@@ -1229,16 +1343,19 @@ int spmm_boo_stage_copy(const spmm_boo_stage* st, int32_t* tiles, uint16_t* tile
               put(crow_ptr, s.crow_ptr.data(), s.crow_ptr.size() * 4) &&
               put(crow_id, s.crow_id.data(), s.crow_id.size() * 4) &&
               put(ccol, s.ccol.data(), s.ccol.size() * 4) &&
-              put(cval, s.cval.data(), s.cval.size());
+              put(cval, s.cval.data(), s.cval.size()) &&
+              put(gtask, s.gtask.data(), s.gtask.size() * 4) &&
+              put(gtask_ptr, s.gtask_ptr.data(), s.gtask_ptr.size() * 4);
     return ok ? SPMM_OK : fail(SPMM_EINVAL, "null output array for a non-empty staging field");
 }
 
 void spmm_boo_stage_destroy(spmm_boo_stage* st) { delete st; }
 
 size_t spmm_boo_workspace_bytes(const spmm_boo_desc* A, spmm_dtype dtype, int64_t batch, int64_t K) {
-    if (!A || A->n_slots <= 0 || batch <= 0 || K <= 0) return 0;
+    if (!A || batch <= 0 || K <= 0) return 0;
     const size_t es = dtype == SPMM_F64 ? 8 : 4;
-    return (size_t)A->n_slots * (size_t)batch * (size_t)ST_ROWS * (size_t)K * es;
+    const size_t gather = A->n_gtask > 0 ? (size_t)A->n_gtask * (size_t)batch * (size_t)K * es : 0;
+    return boo_ws_slots_bytes(A, es, batch, K) + gather;
 }
 
 int spmm_boo_matmul(const spmm_boo_desc* A, spmm_dtype dtype, const void* X, void* Y,

@@ -110,10 +110,27 @@ def check_stream(A, boo, max_item_nnz=4096, long_thr=256, n_waves=64, group=1, m
     assert np.all(slots[last == 1] >= -1)
     sl = st['splits'].reshape(-1, 4)
     assert st['n_slots'] == (sl[:, 3] - sl[:, 2]).sum() if len(sl) else st['n_slots'] == 0
-    long_rows = st['long_rows']
     lens = np.diff(host['rem_indptr'])
-    assert set(long_rows.tolist()) == set(np.nonzero(lens > long_thr)[0].tolist())
+    check_long(st, host, long_thr, set(np.nonzero(lens > long_thr)[0].tolist()))
     return st
+
+
+def check_long(st, host, long_thr, long_rem):
+    """Long remainder rows: listed for the split-row pass if their slice is
+    in the tile stream, else whole rows of the gather pass.  Gather rows longer
+    than long_thr come last, cut into contiguous chunk tasks."""
+    listed = set(st['long_rows'].tolist())
+    gathered = set(st['crow_id'].tolist())
+    assert listed <= long_rem and long_rem <= listed | gathered and not (listed & gathered)
+    cp, n_long = st['crow_ptr'], st['n_crow_long']
+    n_short = len(st['crow_id']) - n_long
+    assert np.all(np.diff(cp)[:n_short] <= long_thr) and np.all(np.diff(cp)[n_short:] > long_thr)
+    gt, gp = st['gtask'].reshape(-1, 2), st['gtask_ptr']
+    assert len(gp) == n_long + 1 and gp[0] == 0 and gp[-1] == len(gt)
+    for i in range(n_long):
+        t = gt[gp[i]:gp[i + 1]]
+        assert t[0, 0] == cp[n_short + i] and t[-1, 1] == cp[n_short + i + 1]
+        assert np.all(t[1:, 0] == t[:-1, 1]) and np.all(t[:, 1] - t[:, 0] <= 1024) and np.all(t[:, 1] > t[:, 0])
 
 
 @pytest.mark.parametrize('policy', ['keep', 'remainder', 'tail_batch'])
@@ -226,3 +243,15 @@ def test_stream_rejects_bad_group():
     for g in (0, 3, 8):
         with pytest.raises(ValueError, match='group'):
             _core.boo_stage(host, 4096, 256, 8, g)
+
+
+def test_gather_pass_long_rows_are_chunked():
+    # scattered columns everywhere, a few rows far longer than the threshold
+    rng = np.random.default_rng(5)
+    A = sp.random(600, 5000, density=0.002, format='lil', random_state=3, dtype=np.float32)
+    for r, n in ((7, 3000), (300, 1500), (599, 300)):
+        A[r, rng.choice(5000, n, replace=False)] = 1.0
+    A = A.tocsr()
+    boo = S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32)
+    st = check_stream(A, boo, long_thr=256, min_reuse=1.5, group=4)
+    assert st['n_crow_long'] == 3 and len(st['gtask']) // 2 == 3 + 2 + 1

@@ -287,7 +287,7 @@ def test_execution_plan_contract():
         S.boo_matmul(boo, x, execution_plan=plan)          # legacy launch mode
 
 
-def test_split_row_groups_and_long_remainder_rows(monkeypatch):
+def test_split_row_groups_and_long_remainder_rows(monkeypatch, path):
     """Heavy row groups cut into several items (partial sums + fixup pass) and
     long remainder rows (split-row pass), forced with small thresholds."""
     monkeypatch.setattr(SB, 'MAX_ITEM_NNZ', 64)
@@ -306,7 +306,10 @@ def test_split_row_groups_and_long_remainder_rows(monkeypatch):
     boo = S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32,
                        small_block_threshold=40).to('cuda')
     d = boo._gpu_meta.desc
-    assert d['n_splits'] > 0 and d['n_long'] > 0
+    if path == 'tile':
+        assert d['n_splits'] > 0 and d['n_long'] > 0
+    else:   # the same rows as chunked gather rows
+        assert d['n_gtask'] >= d['n_crow_long'] > 0
     for K in (64, 5, 128):
         x = _x((3, 700, K)).cuda()
         check(S.boo_matmul(boo, x), A, x)
@@ -355,6 +358,23 @@ def test_scaled_down_power_law_and_permuted_configs(which, monkeypatch):
     d = boo._gpu_meta.desc
     assert d['n_crow'] > 0
     x = torch.from_numpy(M.dense_x(A.shape[1], K)).cuda()
+    y = S.boo_matmul(boo, x)
+    check(y, A, x)
+    assert torch.equal(S.boo_matmul(boo, x), y)
+
+
+@pytest.mark.parametrize('K', [4, 32, 130])
+def test_long_gather_rows_in_chunks(K, monkeypatch):
+    monkeypatch.setattr(SB, 'MIN_COL_REUSE', 1.5)
+    rng = np.random.default_rng(5)
+    A = sp.random(600, 5000, density=0.002, format='lil', random_state=3, dtype=np.float32)
+    for r, n in ((7, 3000), (300, 1500), (599, 300)):
+        A[r, rng.choice(5000, n, replace=False)] = rng.standard_normal(n).astype(np.float32)
+    A = A.tocsr()
+    boo = S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32).to('cuda')
+    d = boo._gpu_meta.desc
+    assert d['n_crow_long'] == 3 and d['n_gtask'] == 6
+    x = _x((2, 5000, K)).cuda()
     y = S.boo_matmul(boo, x)
     check(y, A, x)
     assert torch.equal(S.boo_matmul(boo, x), y)
