@@ -813,10 +813,19 @@ struct PbrGeom {
     static_assert(F % VEC == 0 && NQ >= 1, "bad PBR tile");
 };
 
+// One wave per stripe and feature tile, software-pipelined one block ahead:
+// while block n is walked from LDS, the X rows of block n+1 and the value of
+// its bit (r, c) -- one per lane -- are in flight into registers, and the
+// metadata of block n+2 behind them.  Every step issues the same loads (the
+// next block is clamped to the stripe's last), so no step waits on a load it
+// issued itself.  Lane (r, l) owns row r of the stripe and the VEC-chunks
+// q*LPR + l of the tile; it walks its row's set bits with ctz, reading the
+// bit's value and its X row slice from LDS.  Dense blocks are never formed.
 template <typename T, typename I, int BR, int KT, int VEC, bool FULL>
 __device__ __forceinline__ void pbr_stripe_body(const PbrArgs<T, I>& a, int stripe, int kt, int b,
-                                                T* tile) {
+                                                T* tiles, T* vals) {
     typedef PbrGeom<T, BR, KT, VEC> G;
+    constexpr int NBITS = BR * BR;
     const int lane = threadIdx.x;
     const int r = lane / G::LPR;
     const int l = lane % G::LPR;
@@ -834,58 +843,108 @@ __device__ __forceinline__ void pbr_stripe_body(const PbrArgs<T, I>& a, int stri
         for (int u = 0; u < VEC; ++u) acc[q][u] = T(0);
 
     const int p0 = a.stripe_ptr[stripe], p1 = a.stripe_ptr[stripe + 1];
-    for (int blk = p0; blk < p1; ++blk) {
-        const uint64_t code = (uint64_t)a.codes[blk];
-        const long long col0 = (long long)a.coords[2 * (size_t)blk + 1];
-        const long long off = (long long)a.offsets[blk];
-        __syncthreads();
+    if (p1 > p0) {
+        const int plast = p1 - 1;
+        // X rows of a block into registers (staging lane mapping: chunk ch of
+        // column c; columns past the matrix load column col0 instead)
+        auto load_x = [&](T (&xr)[G::STAGE_ITERS][VEC], long long col0) {
 #pragma unroll
-        for (int m = 0; m < G::STAGE_ITERS; ++m) {
-            const int idx = m * 64 + lane;
-            const int c = idx / G::CHUNKS;
-            const int ch = idx % G::CHUNKS;
-            const int f = fbase + ch * VEC;
-            if (c < BR && col0 + c < a.cols && (FULL || f < K)) {
-                T x[VEC];
-                load_vec<T, VEC>(Xb + (size_t)(col0 + c) * K + f, x);
-                store_vec<T, VEC>(tile + c * G::STRIDE + ch * VEC, x);
+            for (int m = 0; m < G::STAGE_ITERS; ++m) {
+                const int idx = m * 64 + lane;
+                const int c = min(idx / G::CHUNKS, BR - 1);
+                const int ch = idx % G::CHUNKS;
+                const int f = FULL ? fbase + ch * VEC : min(fbase + ch * VEC, K - VEC);
+                const long long xc = col0 + c < a.cols ? col0 + c : col0;
+                load_vec<T, VEC>(Xb + (size_t)xc * K + f, xr[m]);
             }
+        };
+        // the value of bit `lane` of a block (0 when the bit is clear)
+        auto load_v = [&](uint64_t code, long long off) {
+            const bool set = lane < NBITS && ((code >> lane) & 1ull);
+            const int rank = __popcll(code & ((1ull << (lane & 63)) - 1ull));
+            return set ? a.data[off + rank] : T(0);
+        };
+        uint64_t code_n = (uint64_t)a.codes[p0];
+        long long col_n = (long long)a.coords[2 * (size_t)p0 + 1];
+        long long off_n = (long long)a.offsets[p0];
+        T xr[G::STAGE_ITERS][VEC];
+        load_x(xr, col_n);
+        T vv = load_v(code_n, off_n);
+        const int q1 = min(p0 + 1, plast);
+        uint64_t code_f = (uint64_t)a.codes[q1];
+        long long col_f = (long long)a.coords[2 * (size_t)q1 + 1];
+        long long off_f = (long long)a.offsets[q1];
+        for (int blk = p0, n = 0; blk < p1; ++blk, ++n) {
+            T* tile = tiles + (n & 1) * (BR * G::STRIDE);
+            T* vb = vals + (n & 1) * 64;
+            const uint64_t code = code_n;
+            // (1) block blk's X rows and values to LDS
+#pragma unroll
+            for (int m = 0; m < G::STAGE_ITERS; ++m) {
+                const int idx = m * 64 + lane;
+                const int c = idx / G::CHUNKS;
+                const int ch = idx % G::CHUNKS;
+                if (c < BR && (FULL || fbase + ch * VEC < K)) store_vec<T, VEC>(tile + c * G::STRIDE + ch * VEC, xr[m]);
+            }
+            vb[lane] = vv;
+            wave_lds_fence();
+            // (2) loads for block blk+1, metadata of block blk+2
+            code_n = code_f;
+            col_n = col_f;
+            off_n = off_f;
+            load_x(xr, col_n);
+            vv = load_v(code_n, off_n);
+            const int q2 = min(blk + 2, plast);
+            code_f = (uint64_t)a.codes[q2];
+            col_f = (long long)a.coords[2 * (size_t)q2 + 1];
+            off_f = (long long)a.offsets[q2];
+            // (3) walk block blk
+            if (active) {
+                uint32_t rb = (uint32_t)((code >> (BR * r)) & rowbits);
+                while (rb) {
+                    const int c = __builtin_ctz(rb);
+                    rb &= rb - 1u;
+                    const T v = vb[r * BR + c];
+                    const T* xrow = tile + c * G::STRIDE + l * VEC;
+#pragma unroll
+                    for (int q = 0; q < G::NQ; ++q) {
+                        if (FULL || fbase + (q * G::LPR + l) * VEC < K) {
+                            T x[VEC];
+                            load_vec<T, VEC>(xrow + q * G::LPR * VEC, x);
+#pragma unroll
+                            for (int u = 0; u < VEC; ++u) acc[q][u] += v * x[u];
+                        }
+                    }
+                }
+            }
+            wave_lds_fence();
         }
-        __syncthreads();
-        if (active) {
-            uint32_t rb = (uint32_t)((code >> (BR * r)) & rowbits);
-            const uint64_t below = (r == 0) ? 0ull : (code & ((1ull << (BR * r)) - 1ull));
-            const T* dp = a.data + off + __popcll(below);
-            while (rb) {
-                const int c = __builtin_ctz(rb);
-                rb &= rb - 1u;
-                const T v = *dp++;
-                const T* xr = tile + c * G::STRIDE + l * VEC;
+    }
+    if (!active) return;
+    const long long rs = (long long)a.rem_indptr[row], re = (long long)a.rem_indptr[row + 1];
+    if (re - rs <= a.long_threshold) {
+        // four entries at a time, so four X loads are in flight
+        constexpr int U = 4;
+        for (long long j = rs; j < re; j += U) {
+            long long cj[U];
+            T vj[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const long long jj = j + u < re ? j + u : rs;
+                cj[u] = (long long)a.rem_col_ind[jj];
+                vj[u] = j + u < re ? a.rem_vals[jj] : T(0);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const T* xr = Xb + (size_t)cj[u] * K + fbase + l * VEC;
 #pragma unroll
                 for (int q = 0; q < G::NQ; ++q) {
                     if (FULL || fbase + (q * G::LPR + l) * VEC < K) {
                         T x[VEC];
                         load_vec<T, VEC>(xr + q * G::LPR * VEC, x);
 #pragma unroll
-                        for (int u = 0; u < VEC; ++u) acc[q][u] += v * x[u];
+                        for (int e = 0; e < VEC; ++e) acc[q][e] += vj[u] * x[e];
                     }
-                }
-            }
-        }
-    }
-    if (!active) return;
-    const long long rs = (long long)a.rem_indptr[row], re = (long long)a.rem_indptr[row + 1];
-    if (re - rs <= a.long_threshold) {
-        for (long long j = rs; j < re; ++j) {
-            const T v = a.rem_vals[j];
-            const T* xr = Xb + (size_t)a.rem_col_ind[j] * K + fbase + l * VEC;
-#pragma unroll
-            for (int q = 0; q < G::NQ; ++q) {
-                if (FULL || fbase + (q * G::LPR + l) * VEC < K) {
-                    T x[VEC];
-                    load_vec<T, VEC>(xr + q * G::LPR * VEC, x);
-#pragma unroll
-                    for (int u = 0; u < VEC; ++u) acc[q][u] += v * x[u];
                 }
             }
         }
@@ -900,15 +959,16 @@ __device__ __forceinline__ void pbr_stripe_body(const PbrArgs<T, I>& a, int stri
 template <typename T, typename I, int BR, int KT, int VEC>
 __global__ void __launch_bounds__(64) pbr_stripe_kernel(PbrArgs<T, I> a) {
     typedef PbrGeom<T, BR, KT, VEC> G;
-    __shared__ __attribute__((aligned(16))) T tile[BR * G::STRIDE];
+    __shared__ __attribute__((aligned(16))) T tiles[2 * BR * G::STRIDE];
+    __shared__ __attribute__((aligned(16))) T vals[2 * 64];
     const int stripe = xcd_remap(blockIdx.x, gridDim.x);
     if (stripe >= a.n_stripes) return;
     const int kt = blockIdx.y;
     const int b = blockIdx.z;
     if ((kt + 1) * KT <= a.K) {
-        pbr_stripe_body<T, I, BR, KT, VEC, true>(a, stripe, kt, b, tile);
+        pbr_stripe_body<T, I, BR, KT, VEC, true>(a, stripe, kt, b, tiles, vals);
     } else {
-        pbr_stripe_body<T, I, BR, KT, VEC, false>(a, stripe, kt, b, tile);
+        pbr_stripe_body<T, I, BR, KT, VEC, false>(a, stripe, kt, b, tiles, vals);
     }
 }
 
