@@ -35,6 +35,20 @@ How each function is pinned (tests/test_oracle.py):
   spmm_reference       fp64 product of the ORIGINAL CSR plus the elementwise
                        bound |A|.|X| the tolerance is stated against
                        (tests/torch_fast_spdmm/benchmark/bench_real.py:168-208).
+  hem_similarity       (plain loops, small cases) shared-column counts by set
+                       intersection, checked against a dense A A^T; top-k
+                       and symmetrisation rules spelled out per row.
+  hem_pair_hash        the published SplitMix64 output sequence for seed 0
+                       (its first outputs 0xe220a8397b1dcdaf,
+                       0x6e789e6aa1b965f4) pins the mixing function; symmetry.
+  hem_mutual_max       the reference's known answer
+                       (tests/torch_fast_spdmm/test_boo_optimization.py:
+                       15-29); every returned pair is each other's strict
+                       best by (weight, hash); maximality of the round.
+  hem_labels           (plain loops) group sizes / nnz within the caps,
+                       determinism, reference test expectations
+                       (test_boo.py:193-235); the product's labels equal
+                       these on random matrices.
 """
 
 from __future__ import annotations
@@ -45,7 +59,8 @@ import scipy.sparse as sp
 __all__ = [
     'identity_labels', 'boo_build', 'boo_decode', 'boo_cpu_matmul', 'pbr_build',
     'pbr_canonical', 'pbr_decode', 'pbr_cpu_matmul', 'spmm_reference', 'within_bound',
-    'BOO_FIELDS', 'PBR_FIELDS',
+    'BOO_FIELDS', 'PBR_FIELDS', 'hem_similarity', 'hem_pair_hash', 'hem_mutual_max',
+    'hem_labels',
 ]
 
 BOO_FIELDS = ('row_grp_ptr', 'row_ids', 'col_grp_ptr', 'col_ids', 'blk_row_grp', 'blk_col_grp',
@@ -405,3 +420,141 @@ def within_bound(y, A: sp.csr_matrix, x, rel: float = 1e-5):
     with np.errstate(divide='ignore', invalid='ignore'):
         ratio = np.where(bound > 0, err / np.where(bound > 0, bound, 1), np.where(err > 0, np.inf, 0))
     return (float(ratio.max()) if ratio.size else 0.0), ok
+
+
+# ---------------------------------------------------------------------------
+# HEM clustering (torch_fast_spdmm/clustering.py:128-351), plain loops over
+# Python sets and dicts -- small inputs only.
+# ---------------------------------------------------------------------------
+
+def _row_sets(pat):
+    pat = sp.csr_matrix(pat)
+    return [set(pat.indices[pat.indptr[i]:pat.indptr[i + 1]].tolist()) for i in range(pat.shape[0])]
+
+
+def hem_similarity(pat, hub_degree=1024, topk=32):
+    """dict {(i, j): w}: w = |cols(i) & cols(j)| over columns with at most
+    hub_degree entries, i != j, w > 0; row i keeps its topk entries by
+    (w desc, j asc); then an edge is kept with the larger weight of its two
+    directions if either direction kept it (clustering.py:128-183)."""
+    rows = _row_sets(pat)
+    degree = {}
+    for cols in rows:
+        for c in cols:
+            degree[c] = degree.get(c, 0) + 1
+    light = [{c for c in cols if degree[c] <= hub_degree} for cols in rows]
+    n = len(rows)
+    kept = {}
+    if n <= 1:
+        return kept
+    for i in range(n):
+        cand = []
+        for j in range(n):
+            if j != i:
+                w = len(light[i] & light[j])
+                if w > 0:
+                    cand.append((-w, j))
+        cand.sort()
+        if topk is not None:
+            cand = cand[:topk]
+        for negw, j in cand:
+            kept[(i, j)] = -negw
+    out = {}
+    for (i, j), w in kept.items():
+        w2 = max(w, kept.get((j, i), 0))
+        out[(i, j)] = w2
+        out[(j, i)] = w2
+    return out
+
+
+_M64 = (1 << 64) - 1
+
+
+def _mix64_int(z):
+    z ^= z >> 30
+    z = (z * 0xBF58476D1CE4E5B9) & _M64
+    z ^= z >> 27
+    z = (z * 0x94D049BB133111EB) & _M64
+    return z ^ (z >> 31)
+
+
+def hem_pair_hash(a, b):
+    """Symmetric hash of the pair {a, b} (clustering.py:190-207), Python ints."""
+    lo, hi = min(a, b), max(a, b)
+    return _mix64_int(((lo * 0x9E3779B97F4A7C15) & _M64) ^ ((hi * 0xC2B2AE3D27D4EB4F) & _M64)) >> 1
+
+
+def hem_mutual_max(edges, n, active, size, nnz, max_size=None, max_nnz=None, feasible_first=False):
+    """One mutual-max round (clustering.py:210-267) over edges {(i, j): w}:
+    returns the sorted list of pairs (i, j), i < j."""
+    def fits(i, j):
+        return ((max_size is None or size[i] + size[j] <= max_size) and
+                (max_nnz is None or nnz[i] + nnz[j] <= max_nnz))
+    best = {}
+    for (i, j), w in edges.items():
+        if not (active[i] and active[j]):
+            continue
+        if feasible_first and not fits(i, j):
+            continue
+        key = (w, hem_pair_hash(i, j))
+        if i not in best or key > best[i][0]:
+            best[i] = (key, j)
+    pairs = []
+    for i, (_, j) in best.items():
+        if i < j and j in best and best[j][1] == i and fits(i, j):
+            pairs.append((i, j))
+    return sorted(pairs)
+
+
+def hem_labels(pat, target, max_size=None, max_nnz=None, hub_degree=1024, topk=32,
+               residual_rounds=3, feasible_first=False):
+    """Multilevel HEM labels (clustering.py:270-351), original vertex -> group,
+    before the cap pass and renumbering of cluster_axis."""
+    pat = sp.csr_matrix(pat)
+    n = pat.shape[0]
+    labels = list(range(n))
+    if n <= 1 or target <= 1:
+        return np.array(labels, dtype=np.int64)
+    sets = _row_sets(pat)
+    size = [1] * n
+    nnz = [len(s) for s in sets]
+    levels = 8 * max(1, int(np.ceil(np.log2(target)))) + 16
+    for _ in range(levels):
+        m = len(sets)
+        if m <= 1:
+            break
+        cols = sorted({c for s in sets for c in s})
+        index = {c: k for k, c in enumerate(cols)}
+        level = sp.csr_matrix((np.ones(sum(len(s) for s in sets)),
+                               ([i for i, s in enumerate(sets) for _ in s],
+                                [index[c] for s in sets for c in sorted(s)])), shape=(m, max(len(cols), 1)))
+        edges = hem_similarity(level, hub_degree, topk)
+        if not edges:
+            break
+        active = [True] * m
+        pairs = []
+        for _round in range(residual_rounds):
+            got = hem_mutual_max(edges, m, active, size, nnz, max_size, max_nnz, feasible_first)
+            if not got:
+                break
+            for i, j in got:
+                active[i] = active[j] = False
+            pairs += got
+        if not pairs:
+            break
+        owner = list(range(m))
+        for i, j in pairs:
+            owner[j] = i
+        survivors = [v for v in range(m) if owner[v] == v]
+        rank = {v: k for k, v in enumerate(survivors)}
+        new_id = [rank[owner[v]] for v in range(m)]
+        new_sets = [set() for _ in survivors]
+        new_size = [0] * len(survivors)
+        new_nnz = [0] * len(survivors)
+        for v in range(m):
+            new_sets[new_id[v]] |= sets[v]
+            new_size[new_id[v]] += size[v]
+            new_nnz[new_id[v]] += nnz[v]
+        sets, size, nnz = new_sets, new_size, new_nnz
+        labels = [new_id[x] for x in labels]
+    return np.array(labels, dtype=np.int64)

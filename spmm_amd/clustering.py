@@ -8,8 +8,13 @@ renumbered 0..n_groups-1 in order of first label value.  This follows
 ``cluster_axes`` :512-545, ``_enforce_caps`` :83-121, ``_relabel_consecutive``
 :77-80, ``is_pattern_symmetric`` :58-67, ``_tile_by_permutation`` :70-74.
 
-Implemented methods: identity, random, degree, rcm.  The graph methods (hem,
-graclus, metis) are not built yet and raise NotImplementedError.
+Implemented methods: identity, random, degree, rcm and hem (multilevel
+heavy-edge matching on the shared-column graph, :128-351: similarity graph
+:128-183, pair hash :190-207, mutual-max matching :210-267, coarsening
+:270-351).  hem is deterministic and its labels are bit-exact with the
+reference's, since the BOO built from them must be.  graclus and metis wrap
+third-party packages (torch_cluster, pymetis); without them they raise the
+reference's ImportError, as the reference does.
 """
 
 from __future__ import annotations
@@ -22,7 +27,13 @@ import scipy.sparse as sp
 __all__ = ['cluster_axes', 'cluster_axis', 'CLUSTER_METHODS', 'is_pattern_symmetric']
 
 CLUSTER_METHODS = ('identity', 'random', 'degree', 'rcm', 'hem', 'graclus', 'metis')
-_IMPLEMENTED = ('identity', 'random', 'degree', 'rcm')
+
+# Similarity-graph knobs (clustering.py:33-42): columns with more entries than
+# HUB_DEGREE are ignored when counting shared columns; each row keeps its TOPK
+# heaviest neighbours; the product is formed CHUNK_ROWS rows at a time.
+HUB_DEGREE = 1024
+TOPK = 32
+CHUNK_ROWS = 4096
 
 
 def _pattern(mat) -> sp.csr_matrix:
@@ -91,24 +102,217 @@ def _enforce_caps(labels: np.ndarray, row_nnz: np.ndarray, max_size: Optional[in
     return out
 
 
+# ---------------------------------------------------------------------------
+# heavy-edge matching
+# ---------------------------------------------------------------------------
+
+def _similarity_graph(pat: sp.csr_matrix, hub_degree: int, topk: Optional[int],
+                      chunk_rows: int = CHUNK_ROWS) -> sp.csr_matrix:
+    """Row-row weights W[i, j] = number of non-hub columns rows i and j share
+    (i != j).  Each row keeps its ``topk`` heaviest neighbours (ties: lower
+    column index first), then W = max(W, W^T), so an edge survives if either
+    end kept it.  Rectangular input is fine: W is n x n.  clustering.py:128-183.
+    """
+    n, m = pat.shape
+    if n <= 1:
+        return sp.csr_matrix((n, n), dtype=np.int64)
+    degree = np.bincount(pat.indices, minlength=m)
+    light = np.flatnonzero(degree <= hub_degree)
+    # dropping hub columns (and renumbering the rest) leaves every count of
+    # shared columns unchanged
+    P = pat if light.size == m else pat[:, light]
+    P = sp.csr_matrix((np.ones(P.nnz, dtype=np.int64), P.indices, P.indptr), shape=P.shape)
+    PT = P.T.tocsr()
+    rows, cols, weights = [], [], []
+    for r0 in range(0, n, chunk_rows):
+        r1 = min(r0 + chunk_rows, n)
+        prod = (P[r0:r1] @ PT).tocoo()
+        r, c, w = prod.row.astype(np.int64), prod.col.astype(np.int64), prod.data
+        keep = c != r + r0
+        r, c, w = r[keep], c[keep], w[keep]
+        if topk is not None and r.size:
+            order = np.lexsort((c, -w, r))           # by row, heaviest first, then column
+            r_sorted = r[order]
+            first = np.searchsorted(r_sorted, r_sorted, side='left')
+            order = order[np.arange(order.size) - first < topk]
+            r, c, w = r[order], c[order], w[order]
+        rows.append(r + r0)
+        cols.append(c)
+        weights.append(w)
+    if not rows or sum(x.size for x in rows) == 0:
+        return sp.csr_matrix((n, n), dtype=np.int64)
+    W = sp.coo_matrix((np.concatenate(weights), (np.concatenate(rows), np.concatenate(cols))),
+                      shape=(n, n)).tocsr()
+    W.sum_duplicates()
+    return W.maximum(W.T)
+
+
+_U64 = np.uint64
+
+
+def _mix64(z: np.ndarray) -> np.ndarray:
+    """SplitMix64's output function (Steele, Lea and Flood 2014; constants of
+    Vigna's splitmix64.c), on uint64 arrays, wrapping."""
+    z = z ^ (z >> _U64(30))
+    z = z * _U64(0xBF58476D1CE4E5B9)
+    z = z ^ (z >> _U64(27))
+    z = z * _U64(0x94D049BB133111EB)
+    return z ^ (z >> _U64(31))
+
+
+def _pair_hash(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Symmetric 63-bit hash of the unordered pair {a, b} (clustering.py:190-207):
+    mix64(min * 0x9E3779B97F4A7C15 xor max * 0xC2B2AE3D27D4EB4F) >> 1."""
+    lo = np.minimum(a, b).astype(_U64)
+    hi = np.maximum(a, b).astype(_U64)
+    with np.errstate(over='ignore'):
+        h = _mix64((lo * _U64(0x9E3779B97F4A7C15)) ^ (hi * _U64(0xC2B2AE3D27D4EB4F)))
+    return (h >> _U64(1)).astype(np.int64)
+
+
+def _mutual_max_pairs(graph: sp.csr_matrix, active: np.ndarray, size: np.ndarray,
+                      nnz: np.ndarray, max_size: Optional[int], max_nnz: Optional[int],
+                      feasible_first: bool = False) -> Tuple[np.ndarray, np.ndarray]:
+    """One round of mutual-max matching (clustering.py:210-267).
+
+    Among its edges to active vertices (and, with ``feasible_first``, only
+    those whose merged size / nnz fits the caps) every vertex picks the
+    heaviest, ties broken by the larger pair hash.  Two vertices that picked
+    each other form a pair (left < right); pairs over a cap are then dropped.
+    """
+    n = graph.shape[0]
+    g = graph.tocoo()
+    if g.nnz == 0:
+        return np.empty(0, np.int64), np.empty(0, np.int64)
+    r, c, w = g.row.astype(np.int64), g.col.astype(np.int64), g.data
+    live = active[r] & active[c]
+    if feasible_first:
+        if max_size is not None:
+            live &= size[r] + size[c] <= max_size
+        if max_nnz is not None:
+            live &= nnz[r] + nnz[c] <= max_nnz
+    r, c, w = r[live], c[live], w[live]
+    if r.size == 0:
+        return np.empty(0, np.int64), np.empty(0, np.int64)
+    order = np.lexsort((-_pair_hash(r, c), -w, r))
+    r, c = r[order], c[order]
+    head = np.ones(r.size, dtype=bool)
+    head[1:] = r[1:] != r[:-1]
+    choice = np.full(n, -1, dtype=np.int64)
+    choice[r[head]] = c[head]
+    v = np.arange(n, dtype=np.int64)
+    other = np.where(choice >= 0, choice, v)
+    mutual = (choice >= 0) & (choice[other] == v)
+    left = v[mutual & (v < other)]
+    right = other[left]
+    if left.size:
+        fits = np.ones(left.size, dtype=bool)
+        if max_size is not None:
+            fits &= size[left] + size[right] <= max_size
+        if max_nnz is not None:
+            fits &= nnz[left] + nnz[right] <= max_nnz
+        left, right = left[fits], right[fits]
+    return left, right
+
+
+def _hem_labels(pat: sp.csr_matrix, target: int, max_size: Optional[int], max_nnz: Optional[int],
+                hub_degree: int, topk: Optional[int], exact_recompute: bool = True,
+                residual_rounds: int = 3, feasible_first: bool = False,
+                hierarchy: Optional[list] = None) -> np.ndarray:
+    """Multilevel heavy-edge matching (clustering.py:270-351).
+
+    Each level rebuilds the similarity graph of the current supervertices (a
+    supervertex's columns are the union of its members'), runs up to
+    ``residual_rounds`` mutual-max rounds over the still-unmatched vertices,
+    and contracts every pair: the right vertex joins the left one, and the
+    surviving vertices are renumbered in index order.  Levels repeat until one
+    matches nothing (at most 8 ceil(log2 target) + 16 levels); the size / nnz
+    caps bound the growth.  ``hierarchy`` (a list) receives the labels of
+    every level, identity first.
+    """
+    n = pat.shape[0]
+    labels = np.arange(n, dtype=np.int64)
+    if hierarchy is not None:
+        hierarchy.append(labels.copy())
+    if n <= 1 or target <= 1:
+        return labels
+    size = np.ones(n, dtype=np.int64)
+    nnz = np.diff(pat.indptr).astype(np.int64)
+    level = pat
+    graph = None
+    for _ in range(8 * max(1, int(np.ceil(np.log2(target)))) + 16):
+        n_cur = level.shape[0]
+        if n_cur <= 1:
+            break
+        if exact_recompute or graph is None:
+            graph = _similarity_graph(level, hub_degree, topk)
+        if graph.nnz == 0:
+            break
+        active = np.ones(n_cur, dtype=bool)
+        lefts, rights = [], []
+        for _round in range(residual_rounds):
+            left, right = _mutual_max_pairs(graph, active, size, nnz, max_size, max_nnz,
+                                            feasible_first)
+            if left.size == 0:
+                break
+            lefts.append(left)
+            rights.append(right)
+            active[left] = False
+            active[right] = False
+        if not lefts:
+            break
+        left, right = np.concatenate(lefts), np.concatenate(rights)
+        owner = np.arange(n_cur, dtype=np.int64)
+        owner[right] = left                          # pairs are disjoint: one step
+        survivor = owner == np.arange(n_cur)
+        new_index = np.cumsum(survivor) - 1          # survivors keep their order
+        new_id = new_index[owner]
+        n_new = int(survivor.sum())
+        size = np.bincount(new_id, weights=size, minlength=n_new).astype(np.int64)
+        nnz = np.bincount(new_id, weights=nnz, minlength=n_new).astype(np.int64)
+        labels = new_id[labels]
+        if hierarchy is not None:
+            hierarchy.append(labels.copy())
+        merge = sp.csr_matrix((np.ones(n_cur, dtype=np.int64), (new_id, np.arange(n_cur))),
+                              shape=(n_new, n_cur))
+        level = merge @ level
+        level.data[:] = 1                            # union of supports, not a count
+        # without exact_recompute the graph is kept for the next level as is
+    return labels
+
+
 def cluster_axis(mat, method: str = 'hem', target: int = 32, max_size: Optional[int] = None,
-                 max_nnz: Optional[int] = None, seed: int = 0, hub_degree: int = 1024,
-                 topk: Optional[int] = 32, exact_recompute: bool = True,
+                 max_nnz: Optional[int] = None, seed: int = 0, hub_degree: int = HUB_DEGREE,
+                 topk: Optional[int] = TOPK, exact_recompute: bool = True,
                  feasible_first: bool = False, hem_hierarchy: Optional[list] = None) -> np.ndarray:
     """Cluster the ROWS of ``mat`` into groups of about ``target`` rows (int32 labels)."""
     if hem_hierarchy is not None and (method != 'hem' or len(hem_hierarchy)):
         raise ValueError('hem_hierarchy must be an empty list with method=hem')
     if method not in CLUSTER_METHODS:
         raise ValueError(f'unknown clustering method {method!r}; expected one of {CLUSTER_METHODS}')
-    if method not in _IMPLEMENTED:
-        raise NotImplementedError(
-            f'clustering method {method!r} is not implemented in spmm_amd yet; '
-            f'use one of {_IMPLEMENTED} or pass row_labels/col_labels')
+    if method == 'graclus':
+        # clustering.py:356-362: the backend is a third-party package
+        try:
+            from torch_cluster import graclus_cluster  # noqa: F401
+        except (ImportError, OSError) as exc:
+            raise ImportError("cluster='graclus' requires torch-cluster built for the installed "
+                              "PyTorch version; no HEM fallback is performed") from exc
+        raise NotImplementedError("cluster='graclus' is not implemented in spmm_amd")
+    if method == 'metis':
+        # clustering.py:407-412
+        try:
+            import pymetis  # noqa: F401
+        except ImportError as exc:
+            raise ImportError("cluster='metis' requires pymetis>=2025.2.2; "
+                              "install the metis extra. No HEM fallback is performed") from exc
+        raise NotImplementedError("cluster='metis' is not implemented in spmm_amd")
 
     pat = _pattern(mat)
     n = pat.shape[0]
     row_nnz = np.diff(pat.indptr).astype(np.int64)
     if n == 0:
+        if hem_hierarchy is not None:
+            hem_hierarchy.append(np.zeros(0, dtype=np.int64))
         return np.zeros(0, dtype=np.int32)
 
     if method == 'identity':
@@ -117,6 +321,9 @@ def cluster_axis(mat, method: str = 'hem', target: int = 32, max_size: Optional[
         labels = _tile_by_permutation(np.random.default_rng(seed).permutation(n), n, target)
     elif method == 'degree':
         labels = _tile_by_permutation(np.argsort(row_nnz, kind='stable'), n, target)
+    elif method == 'hem':
+        labels = _hem_labels(pat, target, max_size, max_nnz, hub_degree, topk, exact_recompute,
+                             feasible_first=feasible_first, hierarchy=hem_hierarchy)
     else:  # rcm
         if pat.shape[0] != pat.shape[1]:
             raise ValueError("cluster method 'rcm' requires a square matrix")
@@ -133,8 +340,8 @@ def cluster_axis(mat, method: str = 'hem', target: int = 32, max_size: Optional[
 def cluster_axes(mat, method: str = 'hem', target_nr: int = 32, target_nc: int = 32,
                  max_nr: Optional[int] = None, max_nc: Optional[int] = None,
                  max_block_nnz: Optional[int] = None, seed: int = 0,
-                 symmetric: Optional[bool] = None, hub_degree: int = 1024,
-                 topk: Optional[int] = 32, exact_recompute: bool = True,
+                 symmetric: Optional[bool] = None, hub_degree: int = HUB_DEGREE,
+                 topk: Optional[int] = TOPK, exact_recompute: bool = True,
                  feasible_first: bool = False) -> Tuple[np.ndarray, np.ndarray]:
     """(row_labels, col_labels).  A pattern-symmetric matrix with equal targets
     reuses the row labels for the columns; otherwise columns come from A^T."""

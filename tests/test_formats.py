@@ -237,8 +237,9 @@ def test_clustering_identity_and_symmetric_copy():
     rl, cl = cluster_axes(r2, 'identity', 16, 32)
     assert np.array_equal(rl, O.identity_labels(50, 16))
     assert np.array_equal(cl, O.identity_labels(70, 32))
-    with pytest.raises(NotImplementedError):
-        cluster_axes(m, 'hem', 32, 32)
+    for method, pkg in (('graclus', 'torch-cluster'), ('metis', 'pymetis')):
+        with pytest.raises(ImportError, match=pkg):
+            cluster_axes(m, method, 32, 32)
     with pytest.raises(ValueError):
         cluster_axes(m, 'bogus', 32, 32)
 

@@ -378,3 +378,16 @@ def test_long_gather_rows_in_chunks(K, monkeypatch):
     y = S.boo_matmul(boo, x)
     check(y, A, x)
     assert torch.equal(S.boo_matmul(boo, x), y)
+
+
+@pytest.mark.parametrize('target', [8, 16, 32])
+@pytest.mark.parametrize('shape', [(256, 256), (192, 320)])
+def test_hem_clustered_product(target, shape):
+    """The reference's default clustering (cluster='hem'): non-trivial row and
+    column permutations inside every group."""
+    rng = np.random.default_rng(0)
+    A = sp.random(*shape, density=0.05, format='csr', random_state=0, dtype=np.float32)
+    A.data = rng.standard_normal(A.nnz).astype(np.float32)
+    boo = S.csr_to_boo(A, target_nr=target, target_nc=target).to('cuda')
+    x = _x((2, shape[1], 33)).cuda()
+    check(S.boo_matmul(boo, x), A, x)
