@@ -45,10 +45,12 @@ How each function is pinned (tests/test_oracle.py):
                        (tests/torch_fast_spdmm/test_boo_optimization.py:
                        15-29); every returned pair is each other's strict
                        best by (weight, hash); maximality of the round.
-  hem_labels           (plain loops) group sizes / nnz within the caps,
-                       determinism, reference test expectations
-                       (test_boo.py:193-235); the product's labels equal
-                       these on random matrices.
+  hem_labels           (plain loops) label vectors written by the
+                       reference's own clustering.py
+                       (tests/golden/make_hem_fixtures.py ->
+                       tests/golden/hem_labels.npz, 32 cases incl. caps, hub
+                       pruning and top-k); group sizes / nnz within the caps;
+                       determinism; test_boo.py:193-235 expectations.
 """
 
 from __future__ import annotations

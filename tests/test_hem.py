@@ -197,3 +197,41 @@ def test_hem_is_the_default_and_groups_the_banded_matrix():
     assert rows.max() + 1 < 512 // 4
     boo = S.csr_to_boo(a)                               # default cluster='hem'
     assert (S.boo_to_csr(boo) != a).nnz == 0
+
+
+def _golden_cases():
+    from pathlib import Path
+    import ast
+    path = Path(__file__).resolve().parent / 'golden' / 'hem_labels.npz'
+    z = np.load(path)
+    names = sorted({k.split('__')[0] for k in z.files})
+    out = []
+    for nm in names:
+        shape = tuple(int(v) for v in z[f'{nm}__shape'])
+        indptr, indices = z[f'{nm}__indptr'], z[f'{nm}__indices']
+        A = sp.csr_matrix((np.ones(indices.size), indices, indptr), shape=shape)
+        kw = ast.literal_eval(str(z[f'{nm}__kw']))
+        axes = (z[f'{nm}__axes_rows'], z[f'{nm}__axes_cols']) if f'{nm}__axes_rows' in z.files else None
+        out.append((nm, A, kw, z[f'{nm}__labels'], axes))
+    return out
+
+
+GOLDEN = _golden_cases()
+
+
+@pytest.mark.parametrize('case', GOLDEN, ids=[c[0] for c in GOLDEN])
+def test_hem_labels_equal_reference_vectors(case):
+    """Labels written by the reference's own clustering.py
+    (tests/golden/make_hem_fixtures.py): the product and the oracle both."""
+    name, A, kw, want, axes = case
+    got = C.cluster_axis(A, **kw)
+    assert got.dtype == np.int32 and np.array_equal(got, want)
+    raw = O.hem_labels(C._pattern(A), kw['target'], kw.get('max_size'), kw.get('max_nnz'),
+                       hub_degree=kw.get('hub_degree', 1024), topk=kw.get('topk', 32),
+                       feasible_first=kw['feasible_first'])
+    capped = C._enforce_caps(raw, np.diff(C._pattern(A).indptr), kw.get('max_size'), kw.get('max_nnz'))
+    assert np.array_equal(C._relabel_consecutive(capped), want)
+    if axes is not None:
+        r, c = C.cluster_axes(A, 'hem', kw['target'], kw['target'], kw.get('max_size'),
+                              kw.get('max_size'), feasible_first=kw['feasible_first'])
+        assert np.array_equal(r, axes[0]) and np.array_equal(c, axes[1])
