@@ -28,10 +28,11 @@
 //
 // A slice heavier than max_item_nnz sits alone in its group and is cut at tile
 // boundaries into several items: the first stores Y, the others write partial
-// sums to workspace slots that a fixup pass adds in slot order.  Groups are
-// dealt to workgroups as contiguous ranges of near-equal cost (an optimal
-// min-max split).  Column ids of block tiles point into col_ids; those of
-// remainder tiles are appended after it in the same array.
+// sums to workspace slots that a fixup pass adds in slot order.  Each XCD
+// gets a contiguous share of groups of near-equal cost (an optimal min-max
+// split into workgroup ranges), dealt round-robin to its workgroups.  Column
+// ids of block tiles point into col_ids; those of remainder tiles are
+// appended after it in the same array.
 #pragma once
 
 #include <algorithm>
@@ -561,11 +562,6 @@ private:
         S.tile_rs.insert(S.tile_rs.end(), rs, rs + TILE_RS);
     }
 
-    // Deal groups to workgroups of G waves (contiguous ranges of near-equal
-    // cost), then lay out each wave's stream: for each of its workgroup's
-    // groups, its member's tile of every step.  A slice alone in its group is
-    // cut into items of at most max_item_nnz entries (the first stores Y, the
-    // others partial slots).
     // A slice heavier than max_item_nnz (alone in its group) becomes several
     // items, each a group of its own so that different workgroups run them:
     // a run of its steps with at most max_item_nnz entries (or one step).
@@ -609,6 +605,8 @@ private:
         groups_.swap(out);
     }
 
+    // Deal groups to workgroups of G waves, then lay out each wave's stream:
+    // for each of its workgroup's groups, its member's tile of every step.
     void deal_and_emit(Staged& S) {
         const int ng = (int)groups_.size();
         int nwg = std::max(1, std::min(std::max(want_waves_ / G_, 1), ng));
@@ -650,9 +648,21 @@ private:
         wg_first.push_back(ng);
         S.n_waves = nwg * G_;
         S.wave_tiles.assign(1, 0);
+        // The launch gives XCD x the logical workgroups [x*per, (x+1)*per);
+        // their ranges together are the XCD's contiguous share.  Inside it the
+        // groups are dealt round-robin, so the workgroups running at any one
+        // time hold neighbouring groups, whose shared X rows then come from
+        // the XCD's L2 instead of being fetched again later.
+        std::vector<std::vector<int>> wg_groups(nwg);
+        const int per = (nwg + 7) / 8;
+        for (int w0 = 0; w0 < nwg; w0 += per) {
+            const int w1 = std::min(nwg, w0 + per);
+            for (int gi = wg_first[w0]; gi < wg_first[w1]; ++gi)
+                wg_groups[w0 + (gi - wg_first[w0]) % (w1 - w0)].push_back(gi);
+        }
         for (int w = 0; w < nwg; ++w) {
             for (int m = 0; m < G_; ++m) {
-                for (int gi = wg_first[w]; gi < wg_first[w + 1]; ++gi) {
+                for (int gi : wg_groups[w]) {
                     const Group& g = groups_[gi];
                     const bool real = m < g.n_members;
                     const Slice* sl = real ? &slices_[g.members[m]] : nullptr;

@@ -41,6 +41,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <new>
+#include <type_traits>
 #include <string>
 #include <vector>
 
@@ -243,7 +244,7 @@ __device__ __forceinline__ V ld32(const V* base, uint32_t idx) {
 // and the metadata words of tile tn: six vector loads, the same six whatever
 // the tiles hold (indices are clamped into valid memory instead of
 // branching), so the compiler can count them.
-template <typename T>
+template <typename T, bool CID_PAIRS = false>
 __device__ __forceinline__ void st_issue_far(StFar<T>& fr, const StreamArgs<T>& a, const TileMeta& tm,
                                              int t, const TileMeta& mc, int tn) {
     const int lane = threadIdx.x & 63;
@@ -259,7 +260,10 @@ __device__ __forceinline__ void st_issue_far(StFar<T>& fr, const StreamArgs<T>& 
     fr.c = ld32(reinterpret_cast<const uint16_t*>(a.ent_col), k >> 1);
     fr.rs0 = ld32(a.tile_rs, (uint32_t)t * ST_RS + (uint32_t)lr);
     fr.row = ld32(a.row_ids, (uint32_t)(tm.m.w + min(lr, max(nr - 1, 0))));
-    fr.cid = ld32(a.tcols, (uint32_t)(mc.m.z + min(lane & 31, max(nc - 1, 0))));
+    // column id for lane & 31, or (CID_PAIRS) for lane >> 1: the column a lane
+    // stages in the DMA layout
+    const int cl = CID_PAIRS ? lr : (lane & 31);
+    fr.cid = ld32(a.tcols, (uint32_t)(mc.m.z + min(cl, max(nc - 1, 0))));
     fr.meta = ld32(a.tiles, (uint32_t)ST_WORDS * (uint32_t)tn + (uint32_t)(lane & 7));
 }
 
@@ -561,6 +565,198 @@ __global__ void __launch_bounds__(64 * WG, 4) boo_stream_kernel(StreamArgs<T> a,
         for (int s = 0; s < DF; ++s)
             step(fr[s], nr[s % D], msave[s], msave[(s + DF - D) % DF], tb + s, tb + s - t0, tb + s < t1);
     }
+}
+
+// ---------------------------------------------------------------------------
+// BOO tile stream, float, 64-feature tiles: X tiles staged by LDS DMA.
+//
+// The same stream, steps and barriers as boo_stream_kernel (WG = 4), but each
+// wave's share of the next X tile goes from memory straight to LDS with two
+// global_load_lds_dwordx4 (no registers, no LDS writes), issued last in a
+// step; the next step's s_waitcnt vmcnt(0) before its barrier is then the
+// only wait for it, and counting nothing is needed to be correct.  The LDS
+// tile is chunk-major: chunk pair m (features 8m..8m+7) of column c at byte
+// m*1024 + c*32, so one DMA instruction (64 lanes x 16 bytes) stages chunk
+// pair m of all 32 columns, and lane (r, h) reads the 8 chunks 2m+h of a
+// column at one base plus 1024-byte immediates (conflict-free for
+// neighbouring columns, like the padded layout).
+// ---------------------------------------------------------------------------
+
+struct StDmaLds {
+    float tile[2][8 * 32 * 8];
+    float syn[8 * 32 * 8];                      // wave w's serial rows: columns 8w .. 8w+7
+    NzEntry<float> nzp[4][ST_ENT + ST_SYN];
+    int spare[4];                               // the row pass reads one entry past its range
+};
+
+// Low 32 bits of a generic pointer into LDS: the LDS byte address.
+__device__ __forceinline__ uint32_t lds_u32(const void* p) { return (uint32_t)(uintptr_t)p; }
+
+// 64 lanes x 16 bytes from gbase + voff (per lane) to LDS [ldsa, ldsa + 1 KiB),
+// lane i at ldsa + 16 i.
+__device__ __forceinline__ void dma16(const float* gbase, uint32_t voff, uint32_t ldsa) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(gbase), "s"(ldsa)
+                 : "memory", "m0");
+}
+
+// st_row for the chunk-major tile.
+__device__ __forceinline__ void dma_row(float (&acc)[8][4], int j, int e, const NzEntry<float>* nzp,
+                                        const float* tile, int h) {
+    if (j >= e) return;
+    typedef __attribute__((address_space(3))) const char lds_char;
+    lds_char* tb = (lds_char*)(tile) + h * 16;
+    NzEntry<float> ent = nzp[j];
+#pragma nounroll
+    for (; j < e; ++j) {
+        const NzEntry<float> nxt = nzp[j + 1];
+        __builtin_amdgcn_sched_barrier(0);
+        const float* xr = (const float*)(lds_char*)(tb + __umul24(ent.col, 32u));
+        float x[8][4];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) load_vec<float, 4>(xr + q * 256, x[q]);
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc[q][u] += ent.val * x[q][u];
+        ent = nxt;
+    }
+}
+
+// st_serial for the chunk-major tile: lane f takes feature f; busy row k's
+// sums become column 8 wv + k of the shared syn tile.
+__device__ __forceinline__ void dma_serial(uint64_t busy, int& rs0, int& rs1, NzEntry<float>* nzp,
+                                           const float* tile, float* syn, int wv) {
+    const int lane = threadIdx.x & 63;
+    const int fo = (lane >> 3) * 256 + ((lane >> 2) & 1) * 4 + (lane & 3);  // feature lane's offset
+    const float* xc = tile + fo;
+    const int in0 = rs0, in1 = rs1;
+    for (int k = 0; busy; ++k) {
+        const int l2 = __builtin_ctzll(busy);
+        busy &= busy - 1;
+        int j = __builtin_amdgcn_readlane(in0, l2);
+        const int e = __builtin_amdgcn_readlane(in1, l2);
+        float s0 = 0.f, s1 = 0.f;
+        for (; j + 2 <= e; j += 2) {
+            const NzEntry<float> a0 = nzp[j], a1 = nzp[j + 1];
+            s0 += a0.val * xc[a0.col * 8];
+            s1 += a1.val * xc[a1.col * 8];
+        }
+        if (j < e) {
+            const NzEntry<float> a0 = nzp[j];
+            s0 += a0.val * xc[a0.col * 8];
+        }
+        const int col = 8 * wv + k;
+        syn[fo + col * 8] = s0 + s1;
+        if (lane == 0) nzp[ST_ENT + k] = NzEntry<float>{(uint32_t)col, 1.f};
+        if ((lane & ~1) == l2) {
+            rs0 = ST_ENT + k;
+            rs1 = ST_ENT + k + 1;
+        }
+    }
+}
+
+template <int DF>
+__global__ void __launch_bounds__(256, 4) boo_stream_dma_kernel(StreamArgs<float> a, int kt0) {
+    constexpr int D = 1, WG = 4;
+    static_assert(DF > D && ST_WORDS * (DF + D) <= 64, "bad prefetch depth");
+    __shared__ __attribute__((aligned(16))) StDmaLds L;
+    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int w = xcd_remap(blockIdx.x, gridDim.x) * WG + wv;
+    if (w >= a.n_waves) return;  // uniform per workgroup: n_waves is a multiple of WG
+    const int lane = threadIdx.x & 63;
+    const int h = lane & 1;
+    const int lr = lane >> 1;
+    const int fbase = (kt0 + (int)blockIdx.y) * 64;
+    const int b = blockIdx.z;
+    const float* Xb = a.X + (size_t)b * a.cols * a.K;
+    const int t0 = a.wave_tiles[w], t1 = a.wave_tiles[w + 1];
+    if (t0 >= t1) return;  // uniform per workgroup: its streams have equal lengths
+    const int tl = t1 - 1;
+    auto cl = [tl](int t) { return min(t, tl); };
+    NzEntry<float>* nzp = L.nzp[wv];
+    const uint32_t rowb = (uint32_t)a.K * 4u;
+    const uint32_t lane_off = (uint32_t)fbase * 4u + (uint32_t)h * 16u + (uint32_t)(2 * wv) * 32u;
+    // this wave's DMA instructions stage chunk pairs 2wv and 2wv+1 of column lr
+    auto issue_dma = [&](int cid, int buf) {
+        const uint32_t v = __umul24((uint32_t)cid, rowb) + lane_off;
+        const uint32_t l0 = lds_u32(&L.tile[buf][(2 * wv) * 256]);
+        dma16(Xb, v, l0);
+        dma16(Xb, v + 32u, l0 + 1024u);
+    };
+
+    StFar<float> fr[DF];
+    TileMeta msave[DF];
+    {
+        const int mw = ld32(a.tiles, (uint32_t)ST_WORDS * (uint32_t)cl(t0 + (lane >> 3)) + (uint32_t)(lane & 7));
+        const int4 m0 = meta_of(mw, 0).m;
+        const int cid0 = ld32(a.tcols, (uint32_t)(m0.z + min(lr, max(((m0.y >> 8) & 0xff) - 1, 0))));
+#pragma unroll
+        for (int j = 0; j < DF; ++j)
+            st_issue_far<float, true>(fr[j], a, meta_of(mw, j), cl(t0 + j), meta_of(mw, j + D),
+                                      cl(t0 + j + DF + D));
+        issue_dma(cid0, 0);
+        msave[DF - D] = meta_of(mw, DF);
+    }
+
+    float acc[8][4];
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[q][u] = 0.f;
+
+    auto step = [&](StFar<float>& FR, TileMeta& MS, const TileMeta& MP, int t, int n, bool real) {
+        const int4 mt = FR.m;
+        const int nnz = mt.y & 0xff;
+        const float* tile = L.tile[n & 1];
+        if (2 * lane < nnz) {
+            NzEntry<float>* e = nzp + 2 * lane;
+            e[0] = NzEntry<float>{FR.c & 0xffu, FR.v.x};
+            e[1] = NzEntry<float>{(FR.c >> 8) & 0xffu, FR.v.y};
+        }
+        int rs0 = opaque_copy(FR.rs0);
+        int rs1 = __shfl_down(rs0, 2);          // the next row's start
+        if (lr == ST_ROWS - 1) rs1 = nnz;
+        const int row = opaque_copy(FR.row);
+        const int cidn = opaque_copy(FR.cid);
+        const int slot = FR.slot;
+        const TileMeta mfar = MP;                  // tile t+DF
+        const TileMeta mnew = meta_of(FR.meta);    // tile t+DF+D
+        MS = mnew;
+        __builtin_amdgcn_sched_barrier(0);
+        // every load of the last step has landed (this wave's DMA share of
+        // tile t among them); the barrier publishes the whole tile
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        st_issue_far<float, true>(FR, a, mfar, cl(t + DF), mnew, cl(t + 2 * DF + D));
+        __builtin_amdgcn_sched_barrier(0);
+        issue_dma(cidn, (n + 1) & 1);
+        __builtin_amdgcn_sched_barrier(0);
+        const float* src = tile;
+        if ((mt.y >> 24) & ST_FLAG_SERIAL) {
+            const uint64_t busy = __ballot(h == 0 && rs0 != rs1);
+            dma_serial(busy, rs0, rs1, nzp, tile, L.syn, wv);
+            wave_lds_fence();
+            src = L.syn;
+        }
+        dma_row(acc, rs0, rs1, nzp, src, h);
+        wave_lds_fence();
+        if (real && ((mt.y >> 24) & ST_FLAG_LAST)) {
+            const int nrow = (mt.y >> 16) & 0xff;
+            st_store<float, 32, 4, true>(a, acc, row, slot, nrow, b, fbase);
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+#pragma unroll
+                for (int u = 0; u < 4; ++u) acc[q][u] = 0.f;
+        }
+    };
+
+    for (int tb = t0; tb < t1; tb += DF) {
+#pragma unroll
+        for (int s = 0; s < DF; ++s)
+            step(fr[s], msave[s], msave[(s + DF - D) % DF], tb + s, tb + s - t0, tb + s < t1);
+    }
+    // the last step's DMA lands before the workgroup's LDS is released
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 template <typename T>
@@ -1040,6 +1236,15 @@ int launch_boo_stream_a(const StreamArgs<T>& a, hipStream_t s) {
         hipLaunchKernelGGL(kern, grid, dim3(64 * wg), 0, s, a, kt);
         return check_launch("boo_stream_kernel");
     };
+    if constexpr (std::is_same<T, float>::value && F == 32 && VEC == 4 && A32) {
+        if (wg4 && full > 0) {  // full 64-feature tiles: X staged by LDS DMA
+            const dim3 grid(round_up8(a.n_waves / 4), full, a.batch);
+            hipLaunchKernelGGL((boo_stream_dma_kernel<DF>), grid, dim3(256), 0, s, a, 0);
+            const int rc = check_launch("boo_stream_dma_kernel");
+            if (rc || a.K % (2 * F) == 0) return rc;
+            return go(boo_stream_kernel<T, F, VEC, D, DF, 4, false, A32>, 4, 1, full);
+        }
+    }
     if (full > 0) {
         const int rc = wg4 ? go(boo_stream_kernel<T, F, VEC, D, DF, (NST % 4 == 0 ? 4 : 1), true, A32>, 4, full, 0)
                            : go(boo_stream_kernel<T, F, VEC, D, DF, 1, true, A32>, 1, full, 0);
