@@ -18,6 +18,13 @@
 //    same step; the X tile is then assembled in LDS (row stride padded by
 //    32 bytes so neighbouring columns fall in distinct banks), one barrier
 //    publishes it, and every member reads the columns its rows use.
+//  * boo_stream_dma_kernel -- the same walk for float 64-feature tiles, with
+//    each wave's share of the next X tile copied from memory straight into a
+//    chunk-major LDS tile by global_load_lds_dwordx4 (no staging registers).
+//  * boo_rows_kernel, gather_chunk_kernel, gather_fix_kernel -- the gather
+//    pass: rows whose columns are too scattered for X tiles, a lane group per
+//    row gathering X rows directly; rows over the long-row threshold in
+//    chunk tasks whose partial rows are added in order.
 //  * boo_fixup_kernel -- for row slices too heavy for one item, adds the
 //    partial sums of the extra items into Y in slot order (deterministic).
 //  * rows_long_kernel -- remainder rows longer than the long-row threshold:
