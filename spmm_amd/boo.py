@@ -510,15 +510,24 @@ def boo_arena_bytes(max_nr: int, max_nc: int, max_nnz_blk: int, p: int, scalar_b
 
 
 def _gfx950_lds_bytes(scalar_bytes: int) -> int:
-    """LDS per workgroup of the gfx950 row-group kernel: a 32-column tile of
-    256-byte feature rows padded to 288 bytes, plus a 33-entry row table."""
-    return 32 * 288 + 4 * 33
+    """LDS per workgroup of the gfx950 tile-stream kernel (4 waves, one slice
+    each, sharing a 32-column X tile of 64 features).  float: the LDS-DMA
+    kernel's chunk-major tile, double-buffered, 8 serial-row sums per wave and
+    136 entries per wave.  Other types: the register-staged kernel's padded
+    tile (row stride 64 features + 32 bytes), the same per-wave arrays and a
+    32-entry column table per wave."""
+    entry = 8 if scalar_bytes <= 4 else 16    # {uint32 column, value}, aligned
+    if scalar_bytes == 4:
+        return 2 * 8192 + 8192 + 4 * 136 * entry + 16
+    stride = (64 + 32 // scalar_bytes) * scalar_bytes
+    return 2 * 32 * stride + 4 * 8 * stride + 4 * 136 * entry + 4 * 32 * 4
 
 
 def boo_info(boo_mat, p: int = 64, threads: int = 256, row_seg: bool = True) -> BOOInfo:
     """Structural summary derived from the built format.  ``arena_bytes`` and
-    the occupancy fields describe this library's gfx950 kernel (one 64-lane
-    workgroup per row group), not the reference's CUDA launch."""
+    the occupancy fields describe this library's gfx950 tile-stream kernel
+    (256-lane workgroups of 4 waves, LDS-bound count per CU), not the
+    reference's CUDA launch."""
     scalar_bytes = np.dtype(boo_mat.scalar_dtype).itemsize
     row_grp_ptr = np.asarray(boo_mat.row_grp_ptr, dtype=np.int64)
     col_grp_ptr = np.asarray(boo_mat.col_grp_ptr, dtype=np.int64)
@@ -546,7 +555,7 @@ def boo_info(boo_mat, p: int = 64, threads: int = 256, row_seg: bool = True) -> 
     tail = boo_mat.tail_nnz()
     total = int(boo_mat.total_nnz)
     arena = _gfx950_lds_bytes(scalar_bytes)
-    wgs = max(0, min(_LDS_PER_CU // arena, _MAX_WAVES_PER_CU))
+    wgs = max(0, min(_LDS_PER_CU // arena, _MAX_WAVES_PER_CU // 4))
     return BOOInfo(
         shape=(int(boo_mat.rows), int(boo_mat.cols)), total_nnz=total, compressed_nnz=compressed,
         remainder_nnz=boo_mat.remainder_nnz(), tail_nnz=tail,
@@ -560,4 +569,4 @@ def boo_info(boo_mat, p: int = 64, threads: int = 256, row_seg: bool = True) -> 
         x_loads=x_loads, y_writes=y_writes,
         arithmetic_intensity=compressed / x_loads if x_loads else 0.0,
         scalar_bytes=scalar_bytes, p=p, threads=threads, arena_bytes=arena, ctas_per_sm=wgs,
-        occupancy_pct=100.0 * wgs / _MAX_WAVES_PER_CU)
+        occupancy_pct=100.0 * 4 * wgs / _MAX_WAVES_PER_CU)
