@@ -370,7 +370,11 @@ private:
         auto heavy = [&](int i) { return slices_[i].nnz > max_item_nnz_; };
         std::vector<char> used(ns, 0);
         for (int i = 0; i < ns; ++i) used[i] = slices_[i].csr;
-        std::vector<int> score(ns, 0), touched;
+        // score: group keys a candidate shares; pair: its shared keys summed
+        // over the members (ties on score go to the candidate closest to all
+        // members, which keeps groups compact: a 2x2 block of stencil slices
+        // touches fewer column groups than a line of four)
+        std::vector<int> score(ns, 0), pair(ns, 0), touched;
         std::vector<int> keys;
         int fill = 0;
         for (int i = 0; i < ns; ++i) {
@@ -386,15 +390,16 @@ private:
                 auto add_keys = [&](int s) {
                     for (size_t c = slices_[s].c0; c < slices_[s].c1; ++c) {
                         const int k = chunks_[c].cid_off;
-                        if (std::find(keys.begin(), keys.end(), k) != keys.end()) continue;
-                        keys.push_back(k);
+                        const bool fresh = std::find(keys.begin(), keys.end(), k) == keys.end();
+                        if (fresh) keys.push_back(k);
                         // candidates: the next few slices (in order) that share the key
                         auto it = std::lower_bound(kv.begin(), kv.end(), std::make_pair(k, i));
                         for (int n = 0; it != kv.end() && it->first == k && n < 64; ++it, ++n) {
                             const int o = it->second;
                             if (used[o] || heavy(o)) continue;
-                            if (score[o] == 0) touched.push_back(o);
-                            ++score[o];
+                            if (score[o] == 0 && pair[o] == 0) touched.push_back(o);
+                            score[o] += fresh;
+                            ++pair[o];
                         }
                     }
                 };
@@ -402,8 +407,10 @@ private:
                 while (g.n_members < G_) {
                     int best = -1;
                     for (int o : touched)
-                        if (!used[o] && score[o] > 0 && (best < 0 || score[o] > score[best] ||
-                                                         (score[o] == score[best] && o < best)))
+                        if (!used[o] && score[o] > 0 &&
+                            (best < 0 || score[o] > score[best] ||
+                             (score[o] == score[best] && (pair[o] > pair[best] ||
+                                                          (pair[o] == pair[best] && o < best)))))
                             best = o;
                     if (best < 0) {
                         // nothing shares a chunk: fill with the next free slice,
@@ -416,7 +423,7 @@ private:
                     g.members[g.n_members++] = best;
                     add_keys(best);
                 }
-                for (int o : touched) score[o] = 0;
+                for (int o : touched) score[o] = pair[o] = 0;
             }
             groups_.push_back(g);
         }
