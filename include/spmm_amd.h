@@ -225,6 +225,67 @@ int spmm_csr_naive(const void* indptr, const void* col_ind, const void* vals,
                    spmm_itype itype, spmm_dtype dtype, int64_t rows, int64_t cols,
                    const void* X, void* Y, int64_t K, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Measurement adjuncts.
+ *
+ * C++-timed runs: a timer holds an event pair; a *_timed call records the
+ * start on `stream`, makes exactly the product call named, records the end
+ * and waits for it, and returns the GPU time between the records in *ms --
+ * no host work of the caller's falls inside the interval.  Replaces the
+ * timed_run of the reference's BOOTimedSpMM (bindings/bindings_boo_timed.cu:
+ * 254-270), PBRTimedSpMM (bindings/bindings_pbr_timed.cu:160-180) and
+ * DirectSpMM (bindings/bindings_cusparse.cu:122-134).  A timer serves one
+ * host thread at a time.
+ * ------------------------------------------------------------------------- */
+typedef struct spmm_timer spmm_timer;  /* opaque */
+
+int spmm_timer_create(spmm_timer** out);     /* events created and recorded once */
+void spmm_timer_destroy(spmm_timer* t);
+
+int spmm_boo_matmul_timed(const spmm_boo_desc* A, spmm_dtype dtype,
+                          const void* X, void* Y, int64_t batch, int64_t K,
+                          void* workspace, size_t workspace_bytes, void* stream,
+                          spmm_timer* timer, float* ms);
+int spmm_pbr_matmul_timed(const spmm_pbr_desc* A, spmm_dtype dtype,
+                          const void* X, void* Y, int64_t batch, int64_t K, void* stream,
+                          spmm_timer* timer, float* ms);
+
+/* Vendor baseline: a persistent rocSPARSE generic-SpMM plan, Y = A X with A a
+ * CSR matrix (int32 indices, fp32 values, base 0), X [cols][K] and Y [rows][K]
+ * row-major, alpha 1 and beta 0 (the library writes every element of Y).
+ * Replaces the reference's DirectSpMM over cuSPARSE
+ * (bindings/bindings_cusparse.cu:21-160).  The plan keeps the pointers it is
+ * given; `stream` is its construction stream and the only one run() accepts.
+ * librocsparse is loaded on the first create (SPMM_EUNSUPPORTED when it is
+ * absent).  The workspace (info.workspace_bytes) is the caller's, passed to
+ * preprocess() and kept until destroy(). */
+typedef struct spmm_vendor_spmm spmm_vendor_spmm;  /* opaque */
+
+typedef enum spmm_vendor_alg {
+    SPMM_VENDOR_ALG_DEFAULT = 0,         /* rocsparse_spmm_alg_default */
+    SPMM_VENDOR_ALG_CSR = 1,             /* rocsparse_spmm_alg_csr */
+    SPMM_VENDOR_ALG_CSR_ROW_SPLIT = 2,   /* rocsparse_spmm_alg_csr_row_split */
+    SPMM_VENDOR_ALG_CSR_NNZ_SPLIT = 3,   /* rocsparse_spmm_alg_csr_nnz_split */
+    SPMM_VENDOR_ALG_CSR_MERGE_PATH = 4   /* rocsparse_spmm_alg_csr_merge_path */
+} spmm_vendor_alg;
+
+typedef struct spmm_vendor_info {
+    int32_t version;            /* rocsparse_get_version of the loaded library */
+    int32_t header_version;     /* major*100000 + minor*100 + patch of the headers built against */
+    size_t workspace_bytes;
+    int32_t supported;          /* 0: the library does not implement this SpMM; run() refuses */
+    int32_t preprocess_status;  /* rocsparse_status of the preprocess stage, -1 before it */
+} spmm_vendor_info;
+
+int spmm_vendor_spmm_create(int64_t rows, int64_t cols, int64_t nnz, const int32_t* crow,
+                            const int32_t* col, const float* val, const float* X, int64_t K,
+                            float* Y, int32_t alg, void* stream, spmm_vendor_spmm** out);
+int spmm_vendor_spmm_info(const spmm_vendor_spmm* plan, spmm_vendor_info* info);
+int spmm_vendor_spmm_preprocess(spmm_vendor_spmm* plan, void* workspace, size_t workspace_bytes);
+int spmm_vendor_spmm_run(spmm_vendor_spmm* plan, void* stream);
+int spmm_vendor_spmm_run_timed(spmm_vendor_spmm* plan, void* stream, spmm_timer* timer, float* ms);
+void spmm_vendor_spmm_destroy(spmm_vendor_spmm* plan);
+
 #ifdef __cplusplus
 }
 #endif

@@ -25,6 +25,7 @@ from .pbr import (  # noqa: E402
     pbr_to_csr,
 )
 from .plan import BOOExecutionPlan, prepare_boo_cuda  # noqa: E402
+from .timed import BOOTimedSpMM, DirectSpMM, PBRTimedSpMM  # noqa: E402
 
 __version__ = '0.1.0'
 
@@ -36,4 +37,5 @@ __all__ = [
     'pbr_matmul', 'pbr_batched_matmul_cpu', 'pbr_batched_matmul_cuda',
     'pbr_batched_matmul_chunkcols_cuda', 'pbr_batched_matmul_nnzflat_cuda',
     'pbr_batched_matmul_variant_cuda', 'BOOExecutionPlan', 'prepare_boo_cuda',
+    'BOOTimedSpMM', 'PBRTimedSpMM', 'DirectSpMM',
 ]

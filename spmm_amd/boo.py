@@ -168,6 +168,72 @@ def _merge_tail(rows, rem_indptr, rem_col_ind, rem_vals, tail_row, tail_col, tai
     return indptr, c[order], v[order]
 
 
+def _kernel_staging(rows, cols, d, rowmajor, row_ids_dev, device, rem_dev=None):
+    """The kernel's staging of the BOO arrays ``d`` (the builder's field names,
+    host arrays) on ``device``: the tile stream and gather rows
+    (``spmm_boo_stage_*``) and the remainder CSR with the tail folded in.
+    ``row_ids_dev`` is ``row_ids`` on the device; ``rem_dev`` the remainder CSR
+    already there, when there is no tail to fold in.  Returns (stage tensors,
+    remainder tensors, launch descriptor)."""
+    i32 = np.int32
+    if rowmajor:
+        k_idx, k_val = d['nz_idx'], d['nz_val']
+    else:
+        k_idx, k_val = _rowmajor_copy(np.asarray(d['blk_nz_ptr']), np.asarray(d['nz_idx']),
+                                      np.asarray(d['nz_val']))
+    if np.asarray(d['tail_col']).size:
+        k_rem = _merge_tail(rows, d['rem_indptr'], d['rem_col_ind'], d['rem_vals'],
+                            d['tail_row'], d['tail_col'], d['tail_val'])
+        rem_dev = None
+    else:
+        k_rem = (d['rem_indptr'], d['rem_col_ind'], d['rem_vals'])
+    k_rem_indptr = np.ascontiguousarray(k_rem[0], dtype=i32)
+    k_rem_col = np.ascontiguousarray(k_rem[1], dtype=i32)
+    k_rem_val = np.ascontiguousarray(k_rem[2])
+    n_cu = torch.cuda.get_device_properties(device).multi_processor_count
+    host = {
+        'rows': rows, 'cols': cols,
+        'n_row_groups': int(np.asarray(d['row_grp_ptr']).size) - 1,
+        'n_col_groups': int(np.asarray(d['col_grp_ptr']).size) - 1,
+        'num_blocks': int(np.asarray(d['blk_row_grp']).size),
+        'row_grp_ptr': np.ascontiguousarray(d['row_grp_ptr'], dtype=i32),
+        'row_ids': np.ascontiguousarray(d['row_ids'], dtype=i32),
+        'col_grp_ptr': np.ascontiguousarray(d['col_grp_ptr'], dtype=i32),
+        'col_ids': np.ascontiguousarray(d['col_ids'], dtype=i32),
+        'blk_row_grp': np.ascontiguousarray(d['blk_row_grp'], dtype=i32),
+        'blk_col_grp': np.ascontiguousarray(d['blk_col_grp'], dtype=i32),
+        'blk_nz_ptr': np.ascontiguousarray(d['blk_nz_ptr'], dtype=i32),
+        'blk_shift': np.ascontiguousarray(d['blk_shift'], dtype=np.uint8),
+        'nz_idx': np.ascontiguousarray(k_idx, dtype=np.uint16),
+        'nz_val': np.ascontiguousarray(k_val),
+        'rem_indptr': k_rem_indptr, 'rem_col_ind': k_rem_col, 'rem_vals': k_rem_val,
+    }
+    stage = core.boo_stage(host, MAX_ITEM_NNZ, LONG_ROW_THRESHOLD, max(GROUP, n_cu * WAVES_PER_CU), GROUP,
+                           MIN_COL_REUSE)
+    g = types.SimpleNamespace(**{k: _pinned(stage[k], device) for k in (
+        'tiles', 'tile_rs', 'ent_val', 'ent_col', 'tcols', 'splits', 'long_rows',
+        'wave_tiles', 'crow_ptr', 'crow_id', 'ccol', 'cval', 'gtask', 'gtask_ptr')})
+    if rem_dev is None:
+        rem_dev = (_pinned(k_rem_indptr, device), _pinned(k_rem_col, device), _pinned(k_rem_val, device))
+    torch.cuda.synchronize(device)
+
+    p = lambda t: int(t.data_ptr())  # noqa: E731
+    desc = {
+        'rows': rows, 'cols': cols, 'row_ids': p(row_ids_dev),
+        'n_tiles': int(stage['n_tiles']), 'tiles': p(g.tiles),
+        'tile_rs': p(g.tile_rs), 'ent_val': p(g.ent_val), 'ent_col': p(g.ent_col),
+        'tcols': p(g.tcols), 'n_waves': int(stage['n_waves']), 'group': int(stage['group']),
+        'wave_tiles': p(g.wave_tiles),
+        'n_slots': int(stage['n_slots']), 'n_splits': int(stage['n_splits']), 'splits': p(g.splits),
+        'n_long': int(stage['n_long']), 'long_rows': p(g.long_rows),
+        'n_crow': int(stage['n_crow']), 'crow_ptr': p(g.crow_ptr), 'crow_id': p(g.crow_id),
+        'ccol': p(g.ccol), 'cval': p(g.cval), 'n_crow_long': int(stage['n_crow_long']),
+        'n_gtask': int(stage['n_gtask']), 'gtask': p(g.gtask), 'gtask_ptr': p(g.gtask_ptr),
+        'rem_indptr': p(rem_dev[0]), 'rem_col_ind': p(rem_dev[1]), 'rem_vals': p(rem_dev[2]),
+    }
+    return g, rem_dev, desc
+
+
 def _boo_to(self, device='cuda'):
     device = torch.device('cpu' if device is None else device)
     if device.type not in ('cpu', 'cuda'):
@@ -187,38 +253,6 @@ def _boo_to(self, device='cuda'):
 
     d = self._d
     i32 = np.int32
-    nz_idx, nz_val = d['nz_idx'], d['nz_val']
-    if self.nz_order != BooNzOrder.ROWMAJOR:
-        k_idx, k_val = _rowmajor_copy(d['blk_nz_ptr'], nz_idx, nz_val)
-    else:
-        k_idx, k_val = nz_idx, nz_val
-    if self.tail_nnz():
-        k_rem = _merge_tail(self.rows, d['rem_indptr'], d['rem_col_ind'], d['rem_vals'],
-                            d['tail_row'], d['tail_col'], d['tail_val'])
-    else:
-        k_rem = (d['rem_indptr'], d['rem_col_ind'], d['rem_vals'])
-    k_rem_indptr = np.ascontiguousarray(k_rem[0], dtype=i32)
-    k_rem_col = np.ascontiguousarray(k_rem[1], dtype=i32)
-    k_rem_val = np.ascontiguousarray(k_rem[2])
-    n_cu = torch.cuda.get_device_properties(device).multi_processor_count
-    host = {
-        'rows': int(self.rows), 'cols': int(self.cols), 'n_row_groups': self.num_row_groups(),
-        'n_col_groups': self.num_col_groups(), 'num_blocks': self.num_blocks(),
-        'row_grp_ptr': np.ascontiguousarray(d['row_grp_ptr'], dtype=i32),
-        'row_ids': np.ascontiguousarray(d['row_ids'], dtype=i32),
-        'col_grp_ptr': np.ascontiguousarray(d['col_grp_ptr'], dtype=i32),
-        'col_ids': np.ascontiguousarray(d['col_ids'], dtype=i32),
-        'blk_row_grp': np.ascontiguousarray(d['blk_row_grp'], dtype=i32),
-        'blk_col_grp': np.ascontiguousarray(d['blk_col_grp'], dtype=i32),
-        'blk_nz_ptr': np.ascontiguousarray(d['blk_nz_ptr'], dtype=i32),
-        'blk_shift': np.ascontiguousarray(d['blk_shift'], dtype=np.uint8),
-        'nz_idx': np.ascontiguousarray(k_idx, dtype=np.uint16),
-        'nz_val': np.ascontiguousarray(k_val),
-        'rem_indptr': k_rem_indptr, 'rem_col_ind': k_rem_col, 'rem_vals': k_rem_val,
-    }
-    stage = core.boo_stage(host, MAX_ITEM_NNZ, LONG_ROW_THRESHOLD, max(GROUP, n_cu * WAVES_PER_CU), GROUP,
-                           MIN_COL_REUSE)
-
     # Field names and dtypes of the reference's _gpu_meta (boo.py:72-92) ...
     meta = types.SimpleNamespace(
         row_grp_ptr=_pinned(d['row_grp_ptr'], device, i32),
@@ -229,8 +263,8 @@ def _boo_to(self, device='cuda'):
         blk_col_grp=_pinned(d['blk_col_grp'], device, i32),
         blk_nz_ptr=_pinned(d['blk_nz_ptr'], device, i32),
         blk_shift=_pinned(d['blk_shift'], device, np.uint8),
-        nz_idx=_pinned(np.ascontiguousarray(nz_idx).view(np.int16), device),
-        nz_val=_pinned(nz_val, device),
+        nz_idx=_pinned(np.ascontiguousarray(d['nz_idx']).view(np.int16), device),
+        nz_val=_pinned(d['nz_val'], device),
         rem_indptr=_pinned(d['rem_indptr'], device, i32),
         rem_col_ind=_pinned(d['rem_col_ind'], device, i32),
         rem_vals=_pinned(d['rem_vals'], device),
@@ -238,36 +272,12 @@ def _boo_to(self, device='cuda'):
         tail_col=_pinned(d['tail_col'], device, i32),
         tail_val=_pinned(d['tail_val'], device),
     )
-    # ... plus the kernel's tile stream and gather rows (spmm_boo_stage_*) and
-    # the remainder CSR with the tail folded in, read by the long-row pass.
-    meta.stage = types.SimpleNamespace(**{k: _pinned(stage[k], device) for k in (
-        'tiles', 'tile_rs', 'ent_val', 'ent_col', 'tcols', 'splits', 'long_rows',
-        'wave_tiles', 'crow_ptr', 'crow_id', 'ccol', 'cval', 'gtask', 'gtask_ptr')})
-    if self.tail_nnz():
-        meta.k_rem_indptr = _pinned(k_rem_indptr, device)
-        meta.k_rem_col_ind = _pinned(k_rem_col, device)
-        meta.k_rem_vals = _pinned(k_rem_val, device)
-    else:
-        meta.k_rem_indptr, meta.k_rem_col_ind, meta.k_rem_vals = (
-            meta.rem_indptr, meta.rem_col_ind, meta.rem_vals)
-    torch.cuda.synchronize(device)
-
-    p = lambda t: int(t.data_ptr())  # noqa: E731
-    g = meta.stage
-    meta.desc = {
-        'rows': int(self.rows), 'cols': int(self.cols), 'row_ids': p(meta.row_ids),
-        'n_tiles': int(stage['n_tiles']), 'tiles': p(g.tiles),
-        'tile_rs': p(g.tile_rs), 'ent_val': p(g.ent_val), 'ent_col': p(g.ent_col),
-        'tcols': p(g.tcols), 'n_waves': int(stage['n_waves']), 'group': int(stage['group']),
-        'wave_tiles': p(g.wave_tiles),
-        'n_slots': int(stage['n_slots']), 'n_splits': int(stage['n_splits']), 'splits': p(g.splits),
-        'n_long': int(stage['n_long']), 'long_rows': p(g.long_rows),
-        'n_crow': int(stage['n_crow']), 'crow_ptr': p(g.crow_ptr), 'crow_id': p(g.crow_id),
-        'ccol': p(g.ccol), 'cval': p(g.cval), 'n_crow_long': int(stage['n_crow_long']),
-        'n_gtask': int(stage['n_gtask']), 'gtask': p(g.gtask), 'gtask_ptr': p(g.gtask_ptr),
-        'rem_indptr': p(meta.k_rem_indptr), 'rem_col_ind': p(meta.k_rem_col_ind),
-        'rem_vals': p(meta.k_rem_vals),
-    }
+    # ... plus the kernel's staging (tile stream, gather rows, remainder CSR
+    # with the tail folded in) and its launch descriptor.
+    rem_dev = None if self.tail_nnz() else (meta.rem_indptr, meta.rem_col_ind, meta.rem_vals)
+    meta.stage, (meta.k_rem_indptr, meta.k_rem_col_ind, meta.k_rem_vals), meta.desc = _kernel_staging(
+        int(self.rows), int(self.cols), d, self.nz_order == BooNzOrder.ROWMAJOR, meta.row_ids, device,
+        rem_dev)
     self._gpu_meta = meta
     return self
 

@@ -56,8 +56,9 @@ def _hipcc():
 
 
 def build_hip():
-    src = CSRC / 'spmm_kernels.hip'
-    _run([_hipcc(), *HIPCC_FLAGS, f'-I{INCLUDE}', src, '-o', HIP_LIB])
+    srcs = [CSRC / 'spmm_kernels.hip', CSRC / 'measure.hip']
+    # measure.hip opens librocsparse with dlopen: link libdl only
+    _run([_hipcc(), *HIPCC_FLAGS, f'-I{INCLUDE}', *srcs, '-o', HIP_LIB, '-ldl'])
 
 
 def build_core():

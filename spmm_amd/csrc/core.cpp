@@ -391,8 +391,7 @@ void boo_matmul_gpu(const py::dict& d, int dtype, uintptr_t x, uintptr_t y, int6
                                  ws_bytes, reinterpret_cast<void*>(stream)));
 }
 
-void pbr_matmul_gpu(const py::dict& d, int dtype, uintptr_t x, uintptr_t y, int64_t batch, int64_t K,
-                    uintptr_t stream) {
+spmm_pbr_desc pbr_desc(const py::dict& d) {
     spmm_pbr_desc A{};
     A.rows = d["rows"].cast<int64_t>();
     A.cols = d["cols"].cast<int64_t>();
@@ -411,8 +410,74 @@ void pbr_matmul_gpu(const py::dict& d, int dtype, uintptr_t x, uintptr_t y, int6
     A.n_long = d["n_long"].cast<int32_t>();
     A.long_rows = reinterpret_cast<const int32_t*>(P(d, "long_rows"));
     A.long_threshold = d["long_threshold"].cast<int32_t>();
+    return A;
+}
+
+void pbr_matmul_gpu(const py::dict& d, int dtype, uintptr_t x, uintptr_t y, int64_t batch, int64_t K,
+                    uintptr_t stream) {
+    spmm_pbr_desc A = pbr_desc(d);
     raise_status(spmm_pbr_matmul(&A, (spmm_dtype)dtype, reinterpret_cast<const void*>(x),
                                  reinterpret_cast<void*>(y), batch, K, reinterpret_cast<void*>(stream)));
+}
+
+// ---- measurement adjuncts: timers, C++-timed calls, the vendor SpMM plan ----
+// Handles cross into Python as integers; the Python classes own them.
+
+uintptr_t new_timer() {
+    spmm_timer* t = nullptr;
+    raise_status(spmm_timer_create(&t));
+    return reinterpret_cast<uintptr_t>(t);
+}
+
+float boo_matmul_gpu_timed(const py::dict& d, int dtype, uintptr_t x, uintptr_t y, int64_t batch,
+                           int64_t K, uintptr_t ws, size_t ws_bytes, uintptr_t stream, uintptr_t timer) {
+    spmm_boo_desc A = boo_desc(d);
+    float ms = 0.f;
+    raise_status(spmm_boo_matmul_timed(&A, (spmm_dtype)dtype, reinterpret_cast<const void*>(x),
+                                       reinterpret_cast<void*>(y), batch, K, reinterpret_cast<void*>(ws),
+                                       ws_bytes, reinterpret_cast<void*>(stream),
+                                       reinterpret_cast<spmm_timer*>(timer), &ms));
+    return ms;
+}
+
+float pbr_matmul_gpu_timed(const py::dict& d, int dtype, uintptr_t x, uintptr_t y, int64_t batch, int64_t K,
+                           uintptr_t stream, uintptr_t timer) {
+    spmm_pbr_desc A = pbr_desc(d);
+    float ms = 0.f;
+    raise_status(spmm_pbr_matmul_timed(&A, (spmm_dtype)dtype, reinterpret_cast<const void*>(x),
+                                       reinterpret_cast<void*>(y), batch, K, reinterpret_cast<void*>(stream),
+                                       reinterpret_cast<spmm_timer*>(timer), &ms));
+    return ms;
+}
+
+uintptr_t vendor_create(int64_t rows, int64_t cols, int64_t nnz, uintptr_t crow, uintptr_t col, uintptr_t val,
+                        uintptr_t x, int64_t K, uintptr_t y, int alg, uintptr_t stream) {
+    spmm_vendor_spmm* p = nullptr;
+    raise_status(spmm_vendor_spmm_create(rows, cols, nnz, reinterpret_cast<const int32_t*>(crow),
+                                         reinterpret_cast<const int32_t*>(col),
+                                         reinterpret_cast<const float*>(val), reinterpret_cast<const float*>(x),
+                                         K, reinterpret_cast<float*>(y), alg, reinterpret_cast<void*>(stream), &p));
+    return reinterpret_cast<uintptr_t>(p);
+}
+
+py::dict vendor_info(uintptr_t plan) {
+    spmm_vendor_info inf{};
+    raise_status(spmm_vendor_spmm_info(reinterpret_cast<const spmm_vendor_spmm*>(plan), &inf));
+    py::dict d;
+    d["version"] = inf.version;
+    d["header_version"] = inf.header_version;
+    d["workspace_bytes"] = inf.workspace_bytes;
+    d["supported"] = inf.supported != 0;
+    d["preprocess_status"] = inf.preprocess_status;
+    return d;
+}
+
+float vendor_run_timed(uintptr_t plan, uintptr_t stream, uintptr_t timer) {
+    float ms = 0.f;
+    raise_status(spmm_vendor_spmm_run_timed(reinterpret_cast<spmm_vendor_spmm*>(plan),
+                                            reinterpret_cast<void*>(stream),
+                                            reinterpret_cast<spmm_timer*>(timer), &ms));
+    return ms;
 }
 
 void csr_naive_gpu(uintptr_t indptr, uintptr_t col, uintptr_t vals, int itype, int dtype, int64_t rows,
@@ -448,5 +513,23 @@ PYBIND11_MODULE(_core, m) {
     m.def("boo_matmul_gpu", &boo_matmul_gpu);
     m.def("pbr_matmul_gpu", &pbr_matmul_gpu);
     m.def("csr_naive_gpu", &csr_naive_gpu);
+    m.def("timer_create", &new_timer);
+    m.def("timer_destroy", [](uintptr_t t) { spmm_timer_destroy(reinterpret_cast<spmm_timer*>(t)); });
+    m.def("boo_matmul_gpu_timed", &boo_matmul_gpu_timed);
+    m.def("pbr_matmul_gpu_timed", &pbr_matmul_gpu_timed);
+    m.def("vendor_create", &vendor_create);
+    m.def("vendor_info", &vendor_info);
+    m.def("vendor_preprocess", [](uintptr_t plan, uintptr_t ws, size_t bytes) {
+        raise_status(spmm_vendor_spmm_preprocess(reinterpret_cast<spmm_vendor_spmm*>(plan),
+                                                 reinterpret_cast<void*>(ws), bytes));
+    });
+    m.def("vendor_run", [](uintptr_t plan, uintptr_t stream) {
+        raise_status(spmm_vendor_spmm_run(reinterpret_cast<spmm_vendor_spmm*>(plan),
+                                          reinterpret_cast<void*>(stream)));
+    });
+    m.def("vendor_run_timed", &vendor_run_timed);
+    m.def("vendor_destroy", [](uintptr_t plan) {
+        spmm_vendor_spmm_destroy(reinterpret_cast<spmm_vendor_spmm*>(plan));
+    });
     m.def("version", []() { return std::string(spmm_version()); });
 }

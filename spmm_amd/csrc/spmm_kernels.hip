@@ -54,6 +54,7 @@
 
 #include "spmm_amd.h"
 #include "boo_stage.hpp"
+#include "internal.hpp"
 
 namespace {
 
@@ -68,6 +69,17 @@ int fail(int code, const char* fmt, ...) {
     g_last_error = buf;
     return code;
 }
+
+}  // namespace
+
+namespace spmm_internal {
+int set_error(int code, const char* msg) {
+    g_last_error = msg;
+    return code;
+}
+}  // namespace spmm_internal
+
+namespace {
 
 int check_launch(const char* what) {
     hipError_t e = hipGetLastError();

@@ -105,6 +105,41 @@ def _pinned(arr, device, dtype=None):
     return torch.from_numpy(a).pin_memory().to(device, non_blocking=True)
 
 
+def _kernel_staging(rows, cols, block_rows, block_cols, coords, rem_indptr, meta, device):
+    """The stripe kernel's staging of a PBR matrix whose reference arrays are
+    on ``device`` in ``meta`` (codes, coords, offsets, data, rem_*):
+    ``stripe_ptr`` (each block row's blocks, which csr_to_pbr emits
+    contiguously) and the rows whose remainder is long, from the host copies
+    ``coords`` and ``rem_indptr``.  Returns (stripe_ptr, long_rows, desc)."""
+    coords = np.asarray(coords)
+    nb = coords.size // 2
+    n_stripes = (rows + block_rows - 1) // block_rows if rows else 0
+    stripe_of = coords.astype(np.int64).reshape(-1, 2)[:, 0] // block_rows
+    if nb and np.any(np.diff(stripe_of) < 0):
+        raise ValueError('PBR blocks must be grouped by block row')
+    stripe_ptr = np.zeros(n_stripes + 1, dtype=np.int64)
+    if nb:
+        np.cumsum(np.bincount(stripe_of, minlength=n_stripes), out=stripe_ptr[1:])
+    if stripe_ptr[-1] > np.iinfo(np.int32).max:
+        raise ValueError('PBR block count must fit int32')
+    rem_len = np.diff(np.asarray(rem_indptr, dtype=np.int64))
+    long_rows = np.flatnonzero(rem_len > LONG_ROW_THRESHOLD).astype(np.int32)
+    stripe_t = _pinned(stripe_ptr, device, np.int32)
+    long_t = _pinned(long_rows, device, np.int32)
+    torch.cuda.synchronize(device)
+    p = lambda t: int(t.data_ptr())  # noqa: E731
+    desc = {
+        'rows': rows, 'cols': cols, 'block_rows': block_rows, 'block_cols': block_cols,
+        'num_blocks': nb, 'itype': 1 if coords.dtype == np.int64 else 0,
+        'codes': p(meta.codes), 'coords': p(meta.coords), 'offsets': p(meta.offsets),
+        'data': p(meta.data), 'rem_indptr': p(meta.rem_indptr),
+        'rem_col_ind': p(meta.rem_col_ind), 'rem_vals': p(meta.rem_vals),
+        'stripe_ptr': p(stripe_t), 'n_long': int(long_rows.size),
+        'long_rows': p(long_t), 'long_threshold': LONG_ROW_THRESHOLD,
+    }
+    return stripe_t, long_t, desc
+
+
 def _pbr_to(self, device='cuda'):
     device = torch.device('cpu' if device is None else device)
     if device.type not in ('cpu', 'cuda'):
@@ -121,19 +156,6 @@ def _pbr_to(self, device='cuda'):
         return self
 
     d = self._d
-    nb = self.accounted_blocks()
-    n_stripes = (self.rows + self.block_rows - 1) // self.block_rows if self.rows else 0
-    stripe_of = np.asarray(d['block_coords'], dtype=np.int64).reshape(-1, 2)[:, 0] // self.block_rows
-    if nb and np.any(np.diff(stripe_of) < 0):
-        raise ValueError('PBR blocks must be grouped by block row')
-    stripe_ptr = np.zeros(n_stripes + 1, dtype=np.int64)
-    if nb:
-        np.cumsum(np.bincount(stripe_of, minlength=n_stripes), out=stripe_ptr[1:])
-    if stripe_ptr[-1] > np.iinfo(np.int32).max:
-        raise ValueError('PBR block count must fit int32')
-    rem_len = np.diff(np.asarray(d['remainder_indptr'], dtype=np.int64))
-    long_rows = np.flatnonzero(rem_len > LONG_ROW_THRESHOLD).astype(np.int32)
-
     # Field names and dtypes of the reference's _gpu_meta (__init__.py:27-35) ...
     meta = types.SimpleNamespace(
         codes=_pinned(d['block_codes'], device, np.int64),
@@ -145,20 +167,9 @@ def _pbr_to(self, device='cuda'):
         rem_vals=_pinned(d['remainder_data'], device),
     )
     # ... plus the stripe pointer and the long remainder rows.
-    meta.stripe_ptr = _pinned(stripe_ptr, device, np.int32)
-    meta.long_rows = _pinned(long_rows, device, np.int32)
-    torch.cuda.synchronize(device)
-    p = lambda t: int(t.data_ptr())  # noqa: E731
-    meta.desc = {
-        'rows': int(self.rows), 'cols': int(self.cols), 'block_rows': int(self.block_rows),
-        'block_cols': int(self.block_cols), 'num_blocks': nb,
-        'itype': 1 if np.dtype(self.index_dtype) == np.int64 else 0,
-        'codes': p(meta.codes), 'coords': p(meta.coords), 'offsets': p(meta.offsets),
-        'data': p(meta.data), 'rem_indptr': p(meta.rem_indptr),
-        'rem_col_ind': p(meta.rem_col_ind), 'rem_vals': p(meta.rem_vals),
-        'stripe_ptr': p(meta.stripe_ptr), 'n_long': int(long_rows.size),
-        'long_rows': p(meta.long_rows), 'long_threshold': LONG_ROW_THRESHOLD,
-    }
+    meta.stripe_ptr, meta.long_rows, meta.desc = _kernel_staging(
+        int(self.rows), int(self.cols), int(self.block_rows), int(self.block_cols),
+        d['block_coords'], d['remainder_indptr'], meta, device)
     self._gpu_meta = meta
     return self
 
