@@ -1057,6 +1057,22 @@ __device__ __forceinline__ void pbr_stripe_body(const PbrArgs<T, I>& a, int stri
 #pragma unroll
         for (int u = 0; u < VEC; ++u) acc[q][u] = T(0);
 
+    // This row's remainder: its bounds are loaded first, and the column ids
+    // of its first RU entries behind the first block's loads, so they land
+    // during the block loop (the values are loaded beside the X rows, which
+    // do not wait for them).  Rows longer than long_threshold are left to
+    // rows_long_kernel.
+    constexpr int RU = G::NQ * VEC <= 8 ? 4 : 2;  // remainder entries per round
+    const long long rs = active ? (long long)a.rem_indptr[row] : 0;
+    const long long re = active ? (long long)a.rem_indptr[row + 1] : 0;
+    const bool rem_here = active && re - rs <= a.long_threshold;
+    I rc[RU];  // -1: no entry
+    auto rem_fetch = [&](long long j) {
+#pragma unroll
+        for (int u = 0; u < RU; ++u) rc[u] = rem_here && j + u < re ? a.rem_col_ind[j + u] : I(-1);
+    };
+    auto rem_prefetch = [&]() { rem_fetch(rs); };
+
     const int p0 = a.stripe_ptr[stripe], p1 = a.stripe_ptr[stripe + 1];
     if (p1 > p0) {
         const int plast = p1 - 1;
@@ -1089,6 +1105,7 @@ __device__ __forceinline__ void pbr_stripe_body(const PbrArgs<T, I>& a, int stri
         uint64_t code_f = (uint64_t)a.codes[q1];
         long long col_f = (long long)a.coords[2 * (size_t)q1 + 1];
         long long off_f = (long long)a.offsets[q1];
+        rem_prefetch();
         for (int blk = p0, n = 0; blk < p1; ++blk, ++n) {
             T* tile = tiles + (n & 1) * (BR * G::STRIDE);
             T* vb = vals + (n & 1) * 64;
@@ -1134,36 +1151,41 @@ __device__ __forceinline__ void pbr_stripe_body(const PbrArgs<T, I>& a, int stri
             }
             wave_lds_fence();
         }
+    } else {
+        rem_prefetch();
     }
-    if (!active) return;
-    const long long rs = (long long)a.rem_indptr[row], re = (long long)a.rem_indptr[row + 1];
-    if (re - rs <= a.long_threshold) {
-        // four entries at a time, so four X loads are in flight
-        constexpr int U = 4;
-        for (long long j = rs; j < re; j += U) {
-            long long cj[U];
-            T vj[U];
+
+    // Remainder rounds: the X rows of RU entries in flight together, the
+    // next round's column ids and values fetched behind them.
+    if (rem_here) {
+        for (long long j = rs; j < re; j += RU) {
+            T xj[RU][G::NQ][VEC];
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const long long jj = j + u < re ? j + u : rs;
-                cj[u] = (long long)a.rem_col_ind[jj];
-                vj[u] = j + u < re ? a.rem_vals[jj] : T(0);
-            }
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const T* xr = Xb + (size_t)cj[u] * K + fbase + l * VEC;
+            for (int u = 0; u < RU; ++u) {
+                const T* xr = Xb + (size_t)(rc[u] >= 0 ? rc[u] : 0) * K + fbase + l * VEC;
 #pragma unroll
                 for (int q = 0; q < G::NQ; ++q) {
-                    if (FULL || fbase + (q * G::LPR + l) * VEC < K) {
-                        T x[VEC];
-                        load_vec<T, VEC>(xr + q * G::LPR * VEC, x);
+                    if (rc[u] >= 0 && (FULL || fbase + (q * G::LPR + l) * VEC < K)) {
+                        load_vec<T, VEC>(xr + q * G::LPR * VEC, xj[u][q]);
+                    } else {
 #pragma unroll
-                        for (int e = 0; e < VEC; ++e) acc[q][e] += vj[u] * x[e];
+                        for (int e = 0; e < VEC; ++e) xj[u][q][e] = T(0);
                     }
                 }
             }
+            T vj[RU];
+#pragma unroll
+            for (int u = 0; u < RU; ++u) vj[u] = rc[u] >= 0 ? a.rem_vals[j + u] : T(0);
+            rem_fetch(j + RU);
+#pragma unroll
+            for (int u = 0; u < RU; ++u)
+#pragma unroll
+                for (int q = 0; q < G::NQ; ++q)
+#pragma unroll
+                    for (int e = 0; e < VEC; ++e) acc[q][e] += vj[u] * xj[u][q][e];
         }
     }
+    if (!active) return;
     T* out = a.Y + ((size_t)b * a.rows + row) * K + fbase + l * VEC;
 #pragma unroll
     for (int q = 0; q < G::NQ; ++q) {
