@@ -836,11 +836,21 @@ __global__ void __launch_bounds__(256) boo_rows_kernel(const int* __restrict__ c
     T acc[VEC];
 #pragma unroll
     for (int u = 0; u < VEC; ++u) acc[u] = T(0);
+    // lanes past the row's end repeat the chunk's first entry with value 0;
+    // the next chunk's entries are fetched behind this chunk's gathers
+    auto fetch = [&](int p, int& c, T& v) {
+        const int n = min(LPR, p1 - p);
+        c = p < p1 ? ccol[p + (l < n ? l : 0)] : 0;
+        v = p < p1 && l < n ? cval[p + l] : T(0);
+    };
+    int cn;
+    T vn;
+    fetch(p0, cn, vn);
     for (int p = p0; p < p1; p += LPR) {
         const int n = min(LPR, p1 - p);
-        // lanes past the row's end repeat its first entry with value 0
-        const int c = ccol[p + (l < n ? l : 0)];
-        const T v = l < n ? cval[p + l] : T(0);
+        const int c = cn;
+        const T v = vn;
+        fetch(p + LPR, cn, vn);
         for (int i0 = 0; i0 < n; i0 += U) {
             int ci[U];
             T vi[U];
