@@ -19,8 +19,9 @@
 //    32 bytes so neighbouring columns fall in distinct banks), one barrier
 //    publishes it, and every member reads the columns its rows use.
 //  * boo_stream_dma_kernel -- the same walk for float 64-feature tiles, with
-//    each wave's share of the next X tile copied from memory straight into a
-//    chunk-major LDS tile by global_load_lds_dwordx4 (no staging registers).
+//    each wave's share of the next X tile copied from memory straight into
+//    LDS by global_load_lds_dwordx4 (no staging registers), whole X rows per
+//    instruction.
 //  * boo_rows_kernel, gather_chunk_kernel, gather_fix_kernel -- the gather
 //    pass: rows whose columns are too scattered for X tiles, a lane group per
 //    row gathering X rows directly; rows over the long-row threshold in
@@ -212,7 +213,7 @@ struct StFar {
     uint32_t c;                // their local columns (low byte, next byte)
     int rs0;                   // first entry of this lane's row (the row's end comes from lane+2)
     int row;                   // this lane's row id
-    int cid;                   // lane & 31: column id (lane & 31) of the tile D steps later (clamped to its last)
+    int cid;                   // column id of the column this lane stages in the tile D steps later (clamped to its last)
     int meta;                  // lanes 0-7: metadata word (lane) of the tile DF+D steps later
     int4 m;                    // this tile's metadata words 0-3 (uniform)
     int slot;                  // its word 4: the item's partial slot, -1 for the owner (uniform)
@@ -259,13 +260,14 @@ __device__ __forceinline__ V ld32(const V* base, uint32_t idx) {
     return *reinterpret_cast<const V*>(reinterpret_cast<const char*>(base) + (size_t)(idx * (uint32_t)sizeof(V)));
 }
 
-// Far loads of tile t (metadata tm), the column ids of tile tc (metadata mc)
-// and the metadata words of tile tn: six vector loads, the same six whatever
+// Far loads of tile t (metadata tm), the id of column cl of tile tc (metadata
+// mc; each lane names the column it stages) and the metadata words of tile
+// tn: six vector loads, the same six whatever
 // the tiles hold (indices are clamped into valid memory instead of
 // branching), so the compiler can count them.
-template <typename T, bool CID_PAIRS = false>
+template <typename T>
 __device__ __forceinline__ void st_issue_far(StFar<T>& fr, const StreamArgs<T>& a, const TileMeta& tm,
-                                             int t, const TileMeta& mc, int tn) {
+                                             int t, const TileMeta& mc, int tn, int cl) {
     const int lane = threadIdx.x & 63;
     fr.m = tm.m;
     fr.slot = tm.slot;
@@ -279,9 +281,6 @@ __device__ __forceinline__ void st_issue_far(StFar<T>& fr, const StreamArgs<T>& 
     fr.c = ld32(reinterpret_cast<const uint16_t*>(a.ent_col), k >> 1);
     fr.rs0 = ld32(a.tile_rs, (uint32_t)t * ST_RS + (uint32_t)lr);
     fr.row = ld32(a.row_ids, (uint32_t)(tm.m.w + min(lr, max(nr - 1, 0))));
-    // column id for lane & 31, or (CID_PAIRS) for lane >> 1: the column a lane
-    // stages in the DMA layout
-    const int cl = CID_PAIRS ? lr : (lane & 31);
     fr.cid = ld32(a.tcols, (uint32_t)(mc.m.z + min(cl, max(nc - 1, 0))));
     fr.meta = ld32(a.tiles, (uint32_t)ST_WORDS * (uint32_t)tn + (uint32_t)(lane & 7));
 }
@@ -503,7 +502,8 @@ __global__ void __launch_bounds__(64 * WG, 4) boo_stream_kernel(StreamArgs<T> a,
                 st_issue_near<T, F, VEC, NW, FULL, A32>(nr[u], a, colbuf, i0, Xb, fbase);
                 wave_lds_fence();
             }
-            st_issue_far<T>(fr[j], a, meta_of(mw, j), cl(t0 + j), meta_of(mw, j + D), cl(t0 + j + DF + D));
+            st_issue_far<T>(fr[j], a, meta_of(mw, j), cl(t0 + j), meta_of(mw, j + D), cl(t0 + j + DF + D),
+                            lane & 31);
         }
 #pragma unroll
         for (int j = 0; j < D; ++j) msave[(DF - D + j) % DF] = meta_of(mw, DF + j);
@@ -555,7 +555,7 @@ __global__ void __launch_bounds__(64 * WG, 4) boo_stream_kernel(StreamArgs<T> a,
         __builtin_amdgcn_sched_barrier(0);
         // (2) X loads of tile t+D; far loads of tile t+DF
         st_issue_near<T, F, VEC, NW, FULL, A32>(NR, a, colbuf, i0, Xb, fbase);
-        st_issue_far<T>(FR, a, mfar, cl(t + DF), mnew, cl(t + 2 * DF + D));
+        st_issue_far<T>(FR, a, mfar, cl(t + DF), mnew, cl(t + 2 * DF + D), lane & 31);
         __builtin_amdgcn_sched_barrier(0);
         // (3) tile t (a step past the range recomputes the last tile into an
         // accumulator that is never stored again)
@@ -593,20 +593,26 @@ __global__ void __launch_bounds__(64 * WG, 4) boo_stream_kernel(StreamArgs<T> a,
 // wave's share of the next X tile goes from memory straight to LDS with two
 // global_load_lds_dwordx4 (no registers, no LDS writes), issued last in a
 // step; the next step's s_waitcnt vmcnt(0) before its barrier is then the
-// only wait for it, and counting nothing is needed to be correct.  The LDS
-// tile is chunk-major: chunk pair m (features 8m..8m+7) of column c at byte
-// m*1024 + c*32, so one DMA instruction (64 lanes x 16 bytes) stages chunk
-// pair m of all 32 columns, and lane (r, h) reads the 8 chunks 2m+h of a
-// column at one base plus 1024-byte immediates (conflict-free for
-// neighbouring columns, like the padded layout).
+// only wait for it, and counting nothing is needed to be correct.  DMA
+// instruction I (of 8) stages columns I, I+8, I+16 and I+24 as whole 256-byte
+// feature rows, 16 neighbouring lanes per row, so it reads 8 whole lines; its
+// 1 KiB block starts at I * DMA_BLK, and the 32 bytes of padding per block put
+// columns that differ mod 8 on distinct banks.  Lane (r, h) reads the 8
+// chunks 2m+h of a column at one base plus 32-byte immediates.
 // ---------------------------------------------------------------------------
 
+constexpr int DMA_BLK = 1056;  // bytes between DMA instruction blocks (1 KiB + 32)
 struct StDmaLds {
-    float tile[2][8 * 32 * 8];
-    float syn[8 * 32 * 8];                      // wave w's serial rows: columns 8w .. 8w+7
+    float tile[2][8 * DMA_BLK / 4];
+    float syn[8 * DMA_BLK / 4];                 // wave w's serial rows: columns 8w .. 8w+7
     NzEntry<float> nzp[4][ST_ENT + ST_SYN];
     int spare[4];                               // the row pass reads one entry past its range
 };
+
+// LDS byte offset of column c of a tile: DMA instruction I = c % 8 holds
+// columns I, I+8, I+16, I+24, each as a whole 256-byte feature row (16
+// neighbouring lanes per row: whole lines), blocks DMA_BLK apart.
+__device__ __forceinline__ uint32_t dma_col_off(uint32_t c) { return (c & 7u) * (uint32_t)DMA_BLK + ((c >> 3) << 8); }
 
 // Low 32 bits of a generic pointer into LDS: the LDS byte address.
 __device__ __forceinline__ uint32_t lds_u32(const void* p) { return (uint32_t)(uintptr_t)p; }
@@ -618,7 +624,7 @@ __device__ __forceinline__ void dma16(const float* gbase, uint32_t voff, uint32_
                  : "memory", "m0");
 }
 
-// st_row for the chunk-major tile.
+// st_row for the DMA tile: entries carry their column's LDS byte offset.
 __device__ __forceinline__ void dma_row(float (&acc)[8][4], int j, int e, const NzEntry<float>* nzp,
                                         const float* tile, int h) {
     if (j >= e) return;
@@ -629,10 +635,10 @@ __device__ __forceinline__ void dma_row(float (&acc)[8][4], int j, int e, const 
     for (; j < e; ++j) {
         const NzEntry<float> nxt = nzp[j + 1];
         __builtin_amdgcn_sched_barrier(0);
-        const float* xr = (const float*)(lds_char*)(tb + __umul24(ent.col, 32u));
+        const float* xr = (const float*)(lds_char*)(tb + ent.col);
         float x[8][4];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) load_vec<float, 4>(xr + q * 256, x[q]);
+        for (int q = 0; q < 8; ++q) load_vec<float, 4>(xr + q * 8, x[q]);
 #pragma unroll
         for (int q = 0; q < 8; ++q)
 #pragma unroll
@@ -641,12 +647,12 @@ __device__ __forceinline__ void dma_row(float (&acc)[8][4], int j, int e, const 
     }
 }
 
-// st_serial for the chunk-major tile: lane f takes feature f; busy row k's
+// st_serial for the DMA tile: lane f takes feature f; busy row k's
 // sums become column 8 wv + k of the shared syn tile.
 __device__ __forceinline__ void dma_serial(uint64_t busy, int& rs0, int& rs1, NzEntry<float>* nzp,
                                            const float* tile, float* syn, int wv) {
     const int lane = threadIdx.x & 63;
-    const int fo = (lane >> 3) * 256 + ((lane >> 2) & 1) * 4 + (lane & 3);  // feature lane's offset
+    const int fo = lane;  // feature lane's offset (floats) inside a column's row
     const float* xc = tile + fo;
     const int in0 = rs0, in1 = rs1;
     for (int k = 0; busy; ++k) {
@@ -657,16 +663,16 @@ __device__ __forceinline__ void dma_serial(uint64_t busy, int& rs0, int& rs1, Nz
         float s0 = 0.f, s1 = 0.f;
         for (; j + 2 <= e; j += 2) {
             const NzEntry<float> a0 = nzp[j], a1 = nzp[j + 1];
-            s0 += a0.val * xc[a0.col * 8];
-            s1 += a1.val * xc[a1.col * 8];
+            s0 += a0.val * xc[a0.col >> 2];
+            s1 += a1.val * xc[a1.col >> 2];
         }
         if (j < e) {
             const NzEntry<float> a0 = nzp[j];
-            s0 += a0.val * xc[a0.col * 8];
+            s0 += a0.val * xc[a0.col >> 2];
         }
-        const int col = 8 * wv + k;
-        syn[fo + col * 8] = s0 + s1;
-        if (lane == 0) nzp[ST_ENT + k] = NzEntry<float>{(uint32_t)col, 1.f};
+        const uint32_t col = dma_col_off(8 * wv + k);
+        syn[fo + (col >> 2)] = s0 + s1;
+        if (lane == 0) nzp[ST_ENT + k] = NzEntry<float>{col, 1.f};
         if ((lane & ~1) == l2) {
             rs0 = ST_ENT + k;
             rs1 = ST_ENT + k + 1;
@@ -694,13 +700,18 @@ __global__ void __launch_bounds__(256, 4) boo_stream_dma_kernel(StreamArgs<float
     auto cl = [tl](int t) { return min(t, tl); };
     NzEntry<float>* nzp = L.nzp[wv];
     const uint32_t rowb = (uint32_t)a.K * 4u;
-    const uint32_t lane_off = (uint32_t)fbase * 4u + (uint32_t)h * 16u + (uint32_t)(2 * wv) * 32u;
-    // this wave's DMA instructions stage chunk pairs 2wv and 2wv+1 of column lr
+    // this wave's DMA instructions I = 2wv, 2wv+1 stage columns I + 8 (lane / 16),
+    // chunk lane % 16; a lane loads the column id of one of its two columns
+    // (scol) and takes the other from its neighbour lane ^ 1
+    const int scol = 2 * wv + 8 * (lane >> 4) + (lane & 1);
+    const uint32_t lane_off = (uint32_t)fbase * 4u + (uint32_t)(lane & 15) * 16u;
+    const bool odd = (lane & 1) != 0;
     auto issue_dma = [&](int cid, int buf) {
-        const uint32_t v = __umul24((uint32_t)cid, rowb) + lane_off;
-        const uint32_t l0 = lds_u32(&L.tile[buf][(2 * wv) * 256]);
-        dma16(Xb, v, l0);
-        dma16(Xb, v + 32u, l0 + 1024u);
+        const int oth = __builtin_amdgcn_mov_dpp(cid, 0xB1, 0xF, 0xF, false);  // lane ^ 1
+        const uint32_t c0 = (uint32_t)(odd ? oth : cid), c1 = (uint32_t)(odd ? cid : oth);
+        const uint32_t l0 = lds_u32(&L.tile[buf][0]) + (uint32_t)(2 * wv) * (uint32_t)DMA_BLK;
+        dma16(Xb, __umul24(c0, rowb) + lane_off, l0);
+        dma16(Xb, __umul24(c1, rowb) + lane_off, l0 + (uint32_t)DMA_BLK);
     };
 
     StFar<float> fr[DF];
@@ -708,11 +719,11 @@ __global__ void __launch_bounds__(256, 4) boo_stream_dma_kernel(StreamArgs<float
     {
         const int mw = ld32(a.tiles, (uint32_t)ST_WORDS * (uint32_t)cl(t0 + (lane >> 3)) + (uint32_t)(lane & 7));
         const int4 m0 = meta_of(mw, 0).m;
-        const int cid0 = ld32(a.tcols, (uint32_t)(m0.z + min(lr, max(((m0.y >> 8) & 0xff) - 1, 0))));
+        const int cid0 = ld32(a.tcols, (uint32_t)(m0.z + min(scol, max(((m0.y >> 8) & 0xff) - 1, 0))));
 #pragma unroll
         for (int j = 0; j < DF; ++j)
-            st_issue_far<float, true>(fr[j], a, meta_of(mw, j), cl(t0 + j), meta_of(mw, j + D),
-                                      cl(t0 + j + DF + D));
+            st_issue_far<float>(fr[j], a, meta_of(mw, j), cl(t0 + j), meta_of(mw, j + D),
+                                cl(t0 + j + DF + D), scol);
         issue_dma(cid0, 0);
         msave[DF - D] = meta_of(mw, DF);
     }
@@ -729,8 +740,8 @@ __global__ void __launch_bounds__(256, 4) boo_stream_dma_kernel(StreamArgs<float
         const float* tile = L.tile[n & 1];
         if (2 * lane < nnz) {
             NzEntry<float>* e = nzp + 2 * lane;
-            e[0] = NzEntry<float>{FR.c & 0xffu, FR.v.x};
-            e[1] = NzEntry<float>{(FR.c >> 8) & 0xffu, FR.v.y};
+            e[0] = NzEntry<float>{dma_col_off(FR.c & 0xffu), FR.v.x};
+            e[1] = NzEntry<float>{dma_col_off((FR.c >> 8) & 0xffu), FR.v.y};
         }
         int rs0 = opaque_copy(FR.rs0);
         int rs1 = __shfl_down(rs0, 2);          // the next row's start
@@ -746,7 +757,7 @@ __global__ void __launch_bounds__(256, 4) boo_stream_dma_kernel(StreamArgs<float
         // tile t among them); the barrier publishes the whole tile
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
-        st_issue_far<float, true>(FR, a, mfar, cl(t + DF), mnew, cl(t + 2 * DF + D));
+        st_issue_far<float>(FR, a, mfar, cl(t + DF), mnew, cl(t + 2 * DF + D), scol);
         __builtin_amdgcn_sched_barrier(0);
         issue_dma(cidn, (n + 1) & 1);
         __builtin_amdgcn_sched_barrier(0);
