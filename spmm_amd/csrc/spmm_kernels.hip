@@ -1019,6 +1019,18 @@ __global__ void __launch_bounds__(256) rows_long_kernel(const int* __restrict__ 
 // PBR: stripe owner
 // ---------------------------------------------------------------------------
 
+// &Xb[col][f] (row length K): a 32-bit byte offset (A32: one batch's X is
+// under 4 GiB) or a 64-bit element offset.
+template <typename T, bool A32>
+__device__ __forceinline__ const T* x_at(const T* Xb, long long col, int K, int f) {
+    if constexpr (A32) {
+        const uint32_t off = (uint32_t)col * ((uint32_t)K * (uint32_t)sizeof(T)) + (uint32_t)f * (uint32_t)sizeof(T);
+        return reinterpret_cast<const T*>(reinterpret_cast<const char*>(Xb) + off);
+    } else {
+        return Xb + (size_t)col * K + f;
+    }
+}
+
 template <typename T, typename I>
 struct PbrArgs {
     long long rows, cols;
@@ -1044,7 +1056,7 @@ struct PbrGeom {
     static constexpr int F = KT / LPR;
     static constexpr int NQ = F / VEC;
     static constexpr int CHUNKS = KT / VEC;
-    static constexpr int STRIDE = KT + 32 / (int)sizeof(T);
+    static constexpr int STRIDE = KT + 32 / (int)sizeof(T);  // LDS row stride (elements), padded 32 B
     static constexpr int STAGE_ITERS = (BR * CHUNKS + 63) / 64;
     static_assert(F % VEC == 0 && NQ >= 1, "bad PBR tile");
 };
@@ -1057,7 +1069,7 @@ struct PbrGeom {
 // issued itself.  Lane (r, l) owns row r of the stripe and the VEC-chunks
 // q*LPR + l of the tile; it walks its row's set bits with ctz, reading the
 // bit's value and its X row slice from LDS.  Dense blocks are never formed.
-template <typename T, typename I, int BR, int KT, int VEC, bool FULL>
+template <typename T, typename I, int BR, int KT, int VEC, bool FULL, bool A32>
 __device__ __forceinline__ void pbr_stripe_body(const PbrArgs<T, I>& a, int stripe, int kt, int b,
                                                 T* tiles, T* vals) {
     typedef PbrGeom<T, BR, KT, VEC> G;
@@ -1107,7 +1119,7 @@ __device__ __forceinline__ void pbr_stripe_body(const PbrArgs<T, I>& a, int stri
                 const int ch = idx % G::CHUNKS;
                 const int f = FULL ? fbase + ch * VEC : min(fbase + ch * VEC, K - VEC);
                 const long long xc = col0 + c < a.cols ? col0 + c : col0;
-                load_vec<T, VEC>(Xb + (size_t)xc * K + f, xr[m]);
+                load_vec<T, VEC>(x_at<T, A32>(Xb, xc, K, f), xr[m]);
             }
         };
         // the value of bit `lane` of a block (0 when the bit is clear)
@@ -1181,17 +1193,15 @@ __device__ __forceinline__ void pbr_stripe_body(const PbrArgs<T, I>& a, int stri
     if (rem_here) {
         for (long long j = rs; j < re; j += RU) {
             T xj[RU][G::NQ][VEC];
+            // entries past the row's end load X row 0 (the row has an entry,
+            // so X has rows) and carry the value 0
 #pragma unroll
             for (int u = 0; u < RU; ++u) {
-                const T* xr = Xb + (size_t)(rc[u] >= 0 ? rc[u] : 0) * K + fbase + l * VEC;
+                const long long cu = rc[u] >= 0 ? (long long)rc[u] : 0;
 #pragma unroll
                 for (int q = 0; q < G::NQ; ++q) {
-                    if (rc[u] >= 0 && (FULL || fbase + (q * G::LPR + l) * VEC < K)) {
-                        load_vec<T, VEC>(xr + q * G::LPR * VEC, xj[u][q]);
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < VEC; ++e) xj[u][q][e] = T(0);
-                    }
+                    const int fq = fbase + (q * G::LPR + l) * VEC;
+                    load_vec<T, VEC>(x_at<T, A32>(Xb, cu, K, FULL ? fq : min(fq, K - VEC)), xj[u][q]);
                 }
             }
             T vj[RU];
@@ -1202,8 +1212,9 @@ __device__ __forceinline__ void pbr_stripe_body(const PbrArgs<T, I>& a, int stri
             for (int u = 0; u < RU; ++u)
 #pragma unroll
                 for (int q = 0; q < G::NQ; ++q)
+                    if (FULL || fbase + (q * G::LPR + l) * VEC < K)
 #pragma unroll
-                    for (int e = 0; e < VEC; ++e) acc[q][e] += vj[u] * xj[u][q][e];
+                        for (int e = 0; e < VEC; ++e) acc[q][e] += vj[u] * xj[u][q][e];
         }
     }
     if (!active) return;
@@ -1214,7 +1225,7 @@ __device__ __forceinline__ void pbr_stripe_body(const PbrArgs<T, I>& a, int stri
     }
 }
 
-template <typename T, typename I, int BR, int KT, int VEC>
+template <typename T, typename I, int BR, int KT, int VEC, bool A32>
 __global__ void __launch_bounds__(64) pbr_stripe_kernel(PbrArgs<T, I> a) {
     typedef PbrGeom<T, BR, KT, VEC> G;
     __shared__ __attribute__((aligned(16))) T tiles[2 * BR * G::STRIDE];
@@ -1224,9 +1235,9 @@ __global__ void __launch_bounds__(64) pbr_stripe_kernel(PbrArgs<T, I> a) {
     const int kt = blockIdx.y;
     const int b = blockIdx.z;
     if ((kt + 1) * KT <= a.K) {
-        pbr_stripe_body<T, I, BR, KT, VEC, true>(a, stripe, kt, b, tiles, vals);
+        pbr_stripe_body<T, I, BR, KT, VEC, true, A32>(a, stripe, kt, b, tiles, vals);
     } else {
-        pbr_stripe_body<T, I, BR, KT, VEC, false>(a, stripe, kt, b, tiles, vals);
+        pbr_stripe_body<T, I, BR, KT, VEC, false, A32>(a, stripe, kt, b, tiles, vals);
     }
 }
 
@@ -1495,7 +1506,11 @@ int boo_matmul_t(const spmm_boo_desc* A, const void* Xv, void* Yv, int64_t batch
 template <typename T, typename I, int BR, int KT, int VEC>
 int launch_pbr(const PbrArgs<T, I>& a, int batch, hipStream_t s) {
     const dim3 grid(round_up8(a.n_stripes), (a.K + KT - 1) / KT, batch);
-    hipLaunchKernelGGL((pbr_stripe_kernel<T, I, BR, KT, VEC>), grid, dim3(64), 0, s, a);
+    // 32-bit X offsets when one batch's X is under 4 GiB
+    if ((uint64_t)a.cols * (uint64_t)a.K * sizeof(T) < (1ull << 32))
+        hipLaunchKernelGGL((pbr_stripe_kernel<T, I, BR, KT, VEC, true>), grid, dim3(64), 0, s, a);
+    else
+        hipLaunchKernelGGL((pbr_stripe_kernel<T, I, BR, KT, VEC, false>), grid, dim3(64), 0, s, a);
     return check_launch("pbr_stripe_kernel");
 }
 
