@@ -265,7 +265,7 @@ __device__ __forceinline__ V ld32(const V* base, uint32_t idx) {
 // tn: six vector loads, the same six whatever
 // the tiles hold (indices are clamped into valid memory instead of
 // branching), so the compiler can count them.
-template <typename T>
+template <typename T, bool SKIP = false>
 __device__ __forceinline__ void st_issue_far(StFar<T>& fr, const StreamArgs<T>& a, const TileMeta& tm,
                                              int t, const TileMeta& mc, int tn, int cl) {
     const int lane = threadIdx.x & 63;
@@ -276,11 +276,21 @@ __device__ __forceinline__ void st_issue_far(StFar<T>& fr, const StreamArgs<T>& 
     const int lr = lane >> 1;
     // entries 2*lane, 2*lane+1 (tiles start at even entries; past nnz: padding)
     const uint32_t k = (uint32_t)(tm.m.x + 2 * min(lane, max((nnz - 1) >> 1, 0)));
-    fr.v = *reinterpret_cast<const typename Pair<T>::type*>(
-        reinterpret_cast<const char*>(a.ent_val) + (size_t)(k * (uint32_t)sizeof(T)));
-    fr.c = ld32(reinterpret_cast<const uint16_t*>(a.ent_col), k >> 1);
-    fr.rs0 = ld32(a.tile_rs, (uint32_t)t * ST_RS + (uint32_t)lr);
-    fr.row = ld32(a.row_ids, (uint32_t)(tm.m.w + min(lr, max(nr - 1, 0))));
+    // SKIP (for a kernel that waits for all its loads at every step rather
+    // than counting them): no entries or row starts for an empty tile, row ids
+    // only for the tile that stores its rows -- uniform branches
+    if (!SKIP || nnz > 0) {
+        fr.v = *reinterpret_cast<const typename Pair<T>::type*>(
+            reinterpret_cast<const char*>(a.ent_val) + (size_t)(k * (uint32_t)sizeof(T)));
+        fr.c = ld32(reinterpret_cast<const uint16_t*>(a.ent_col), k >> 1);
+        fr.rs0 = ld32(a.tile_rs, (uint32_t)t * ST_RS + (uint32_t)lr);
+    } else {
+        fr.rs0 = 0;
+    }
+    if (!SKIP || ((tm.m.y >> 24) & ST_FLAG_LAST))
+        fr.row = ld32(a.row_ids, (uint32_t)(tm.m.w + min(lr, max(nr - 1, 0))));
+    else
+        fr.row = 0;
     fr.cid = ld32(a.tcols, (uint32_t)(mc.m.z + min(cl, max(nc - 1, 0))));
     fr.meta = ld32(a.tiles, (uint32_t)ST_WORDS * (uint32_t)tn + (uint32_t)(lane & 7));
 }
@@ -722,8 +732,8 @@ __global__ void __launch_bounds__(256, 4) boo_stream_dma_kernel(StreamArgs<float
         const int cid0 = ld32(a.tcols, (uint32_t)(m0.z + min(scol, max(((m0.y >> 8) & 0xff) - 1, 0))));
 #pragma unroll
         for (int j = 0; j < DF; ++j)
-            st_issue_far<float>(fr[j], a, meta_of(mw, j), cl(t0 + j), meta_of(mw, j + D),
-                                cl(t0 + j + DF + D), scol);
+            st_issue_far<float, true>(fr[j], a, meta_of(mw, j), cl(t0 + j), meta_of(mw, j + D),
+                                      cl(t0 + j + DF + D), scol);
         issue_dma(cid0, 0);
         msave[DF - D] = meta_of(mw, DF);
     }
@@ -757,7 +767,7 @@ __global__ void __launch_bounds__(256, 4) boo_stream_dma_kernel(StreamArgs<float
         // tile t among them); the barrier publishes the whole tile
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
-        st_issue_far<float>(FR, a, mfar, cl(t + DF), mnew, cl(t + 2 * DF + D), scol);
+        st_issue_far<float, true>(FR, a, mfar, cl(t + DF), mnew, cl(t + 2 * DF + D), scol);
         __builtin_amdgcn_sched_barrier(0);
         issue_dma(cidn, (n + 1) & 1);
         __builtin_amdgcn_sched_barrier(0);
