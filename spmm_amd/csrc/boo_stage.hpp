@@ -657,15 +657,29 @@ private:
         S.wave_tiles.assign(1, 0);
         // The launch gives XCD x the logical workgroups [x*per, (x+1)*per);
         // their ranges together are the XCD's contiguous share.  Inside it the
-        // groups are dealt round-robin, so the workgroups running at any one
-        // time hold neighbouring groups, whose shared X rows then come from
-        // the XCD's L2 instead of being fetched again later.
+        // groups are dealt in order, each to the workgroup with the least cost
+        // so far (the lowest index on ties: round-robin when the groups cost
+        // the same), so the workgroups running at any one time hold
+        // neighbouring groups, whose shared X rows then come from the XCD's L2
+        // instead of being fetched again later, and uneven groups still leave
+        // the workgroups' streams within about one group of each other.
         std::vector<std::vector<int>> wg_groups(nwg);
+        std::vector<long long> load(nwg, 0);
         const int per = (nwg + 7) / 8;
+        std::vector<int> order;
         for (int w0 = 0; w0 < nwg; w0 += per) {
             const int w1 = std::min(nwg, w0 + per);
-            for (int gi = wg_first[w0]; gi < wg_first[w1]; ++gi)
-                wg_groups[w0 + (gi - wg_first[w0]) % (w1 - w0)].push_back(gi);
+            order.clear();
+            for (int gi = wg_first[w0]; gi < wg_first[w1]; ++gi) order.push_back(gi);
+            std::stable_sort(order.begin(), order.end(),
+                             [&](int x, int y) { return groups_[x].cost > groups_[y].cost; });
+            for (int gi : order) {
+                int best = w0;
+                for (int w = w0 + 1; w < w1; ++w)
+                    if (load[w] < load[best]) best = w;
+                wg_groups[best].push_back(gi);
+                load[best] += groups_[gi].cost;
+            }
         }
         for (int w = 0; w < nwg; ++w) {
             for (int m = 0; m < G_; ++m) {
