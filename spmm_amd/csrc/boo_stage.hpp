@@ -62,6 +62,13 @@ constexpr long long COST_ITEM = 512;
 // at most GATHER_CHUNK entries, one workgroup each, into partial rows that a
 // fixup pass adds in chunk order.
 constexpr int GATHER_CHUNK = 1024;
+// When the gather rows' lengths are skewed (standard deviation above the
+// mean, as in a power-law graph), rows longer than GATHER_SKEWED_LONG go to
+// chunk tasks too: there the row pass's waves stall on a few mid-length rows
+// that chunk tasks run wider (R-MAT 2^20, K=128: 2.52 -> 2.18 ms).  With even
+// lengths the chunks' partial rows and fixup cost more than they save (48
+// entries per row: 248 -> 423 us at K=32), so the threshold stays as given.
+constexpr int GATHER_SKEWED_LONG = 32;
 
 
 
@@ -284,11 +291,38 @@ private:
         }
     }
 
+    // Entries of each gather row (block entries plus remainder, long or not),
+    // slice by slice; the long-row threshold of the gather pass follows from
+    // their spread.
+    int gather_long_threshold() const {
+        double s1 = 0.0, s2 = 0.0;
+        long long n = 0;
+        std::vector<long long> cnt;
+        for (const Slice& sl : slices_) {
+            if (!sl.csr) continue;
+            cnt.assign((size_t)sl.nr, 0);
+            for (size_t c = sl.c0; c < sl.c1; ++c)
+                for (size_t e = chunks_[c].e0; e < chunks_[c].e1; ++e) ++cnt[pool_[e].lr];
+            for (size_t e = sl.r0; e < sl.r1; ++e) ++cnt[pool_[e].lr];
+            for (size_t i = sl.g0; i < sl.g1; ++i)
+                cnt[longs_[i].lr] += in_.rem_indptr[longs_[i].row + 1] - in_.rem_indptr[longs_[i].row];
+            for (long long c : cnt) {
+                s1 += (double)c;
+                s2 += (double)c * (double)c;
+            }
+            n += sl.nr;
+        }
+        if (n == 0) return long_threshold_;
+        const double mean = s1 / (double)n, var = s2 / (double)n - mean * mean;
+        return var > mean * mean ? std::min(long_threshold_, GATHER_SKEWED_LONG) : long_threshold_;
+    }
+
     // The gather pass's rows: every row of every slice sent there, whole (its
     // block entries in block order, then its remainder, long or not).  Rows of
-    // at most long_threshold entries come first, in slice order; the longer
-    // ones follow, each cut into chunk tasks.
+    // at most the gather pass's long-row threshold come first, in slice order;
+    // the longer ones follow, each cut into chunk tasks.
     void emit_csr(Staged& S) {
+        const int thr = gather_long_threshold();
         struct RE {
             int32_t lr, col;
             int32_t src;
@@ -321,7 +355,7 @@ private:
                 size_t k1 = k;
                 while (k1 < v.size() && v[k1].lr == lr) ++k1;
                 const int32_t row = in_.row_ids[sl.row_off + lr];
-                const bool is_long = (long long)(k1 - k) > (long long)long_threshold_;
+                const bool is_long = (long long)(k1 - k) > (long long)thr;
                 for (; k < k1; ++k) {
                     const T x = v[k].from_rem ? in_.rem_vals[v[k].src] : in_.nz_val[v[k].src];
                     if (is_long) {

@@ -115,16 +115,26 @@ def check_stream(A, boo, max_item_nnz=4096, long_thr=256, n_waves=64, group=1, m
     return st
 
 
+def gather_threshold(st, long_thr):
+    """The gather pass's long-row threshold: long_thr, or at most 32 when the
+    gather rows' lengths have a standard deviation above their mean."""
+    lens = np.diff(st['crow_ptr']).astype(np.float64)
+    if len(lens) and lens.var() > lens.mean() ** 2:
+        return min(long_thr, 32)
+    return long_thr
+
+
 def check_long(st, host, long_thr, long_rem):
     """Long remainder rows: listed for the split-row pass if their slice is
     in the tile stream, else whole rows of the gather pass.  Gather rows longer
-    than long_thr come last, cut into contiguous chunk tasks."""
+    than the gather threshold come last, cut into contiguous chunk tasks."""
     listed = set(st['long_rows'].tolist())
     gathered = set(st['crow_id'].tolist())
     assert listed <= long_rem and long_rem <= listed | gathered and not (listed & gathered)
     cp, n_long = st['crow_ptr'], st['n_crow_long']
     n_short = len(st['crow_id']) - n_long
-    assert np.all(np.diff(cp)[:n_short] <= long_thr) and np.all(np.diff(cp)[n_short:] > long_thr)
+    thr = gather_threshold(st, long_thr)
+    assert np.all(np.diff(cp)[:n_short] <= thr) and np.all(np.diff(cp)[n_short:] > thr)
     gt, gp = st['gtask'].reshape(-1, 2), st['gtask_ptr']
     assert len(gp) == n_long + 1 and gp[0] == 0 and gp[-1] == len(gt)
     for i in range(n_long):
@@ -260,3 +270,26 @@ def test_gather_pass_long_rows_are_chunked():
     boo = S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32)
     st = check_stream(A, boo, long_thr=256, min_reuse=1.5, group=4)
     assert st['n_crow_long'] == 3 and len(st['gtask']) // 2 == 3 + 2 + 1
+
+
+def test_gather_pass_skewed_rows_chunk_earlier():
+    # power-law-like rows (a few of 40-200 entries among rows of ~3): the rows
+    # above 32 entries become chunk tasks although the threshold is 256
+    rng = np.random.default_rng(11)
+    A = sp.random(2000, 20000, density=0.00015, format='lil', random_state=4, dtype=np.float32)
+    mid = rng.choice(2000, 60, replace=False)
+    for r in mid:
+        A[r, rng.choice(20000, int(rng.integers(40, 200)), replace=False)] = 1.0
+    A = A.tocsr()
+    boo = S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32)
+    st = check_stream(A, boo, long_thr=256, min_reuse=1.5, group=4)
+    lens = np.diff(st['crow_ptr'])
+    assert lens.var() > lens.mean() ** 2
+    assert st['n_crow_long'] == int((np.diff(A.indptr) > 32).sum()) >= 60
+    # even rows of 48 entries: the threshold stays at 256, nothing is chunked
+    n, d = 3000, 48
+    cols = np.stack([rng.choice(20000, d, replace=False) for _ in range(n)]).ravel().astype(np.int32)
+    E = sp.csr_matrix((np.ones(n * d, np.float32), cols, np.arange(0, n * d + 1, d)), shape=(n, 20000))
+    boo = S.csr_to_boo(E, cluster='identity', target_nr=32, target_nc=32)
+    st = check_stream(E, boo, long_thr=256, min_reuse=1.5, group=4)
+    assert len(st['crow_id']) == n and st['n_crow_long'] == 0

@@ -315,6 +315,24 @@ def test_split_row_groups_and_long_remainder_rows(monkeypatch, path):
         check(S.boo_matmul(boo, x), A, x)
 
 
+def test_skewed_gather_rows_as_chunk_tasks(path):
+    """Power-law-like gather rows at the default thresholds: the rows of 40-200
+    entries among rows of ~3 go to chunk tasks (the stage's skewed rule)."""
+    rng = np.random.default_rng(11)
+    A = sp.random(2000, 20000, density=0.00015, format='lil', random_state=4, dtype=np.float32)
+    for r in rng.choice(2000, 60, replace=False):
+        A[r, rng.choice(20000, int(rng.integers(40, 200)), replace=False)] = 1.0
+    A = A.tocsr()
+    A.data = rng.standard_normal(A.nnz).astype(np.float32)
+    boo = S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32).to('cuda')
+    d = boo._gpu_meta.desc
+    if path == 'gather':
+        assert d['n_crow_long'] == int((np.diff(A.indptr) > 32).sum()) >= 60 and d['n_gtask'] >= d['n_crow_long']
+    for K in (32, 128, 5):
+        x = _x((2, 20000, K)).cuda()
+        check(S.boo_matmul(boo, x), A, x)
+
+
 @pytest.mark.parametrize('cfg', [1, 2])
 def test_benchmark_configs_full_size(cfg):
     from spmm_amd import matrices as M
