@@ -131,7 +131,9 @@ int spmm_boo_stage_sizes(const spmm_boo_stage* st, spmm_boo_stage_info* info);
  *   wave_tiles [n_waves+1] int32,
  *   crow_ptr [n_crow+1] int32, crow_id [n_crow] int32, ccol [n_cnz] int32, cval [n_cnz] (dtype):
  *   the rows of the gather pass (Y row ids, their entries with global columns);
- *   the last n_crow_long of them are longer than long_threshold and are summed in
+ *   the last n_crow_long of them are longer than long_threshold (than
+ *   min(long_threshold, 32) when the gather rows' lengths have a standard
+ *   deviation above their mean) and are summed in
  *   chunk tasks: gtask [n_gtask*2] int32 (entry begin, end), gtask_ptr [n_crow_long+1]
  *   int32 (long row i owns tasks gtask_ptr[i] .. gtask_ptr[i+1]).
  * Every tile's entries start at an even index (odd tiles are followed by a
