@@ -16,6 +16,7 @@ Output: one JSON line on stdout (rank 0), as the driver expects.
     python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--config 2]
     python bench.py --calibrate-copy   # plain copy of known size, for rocprof scaling
     python bench.py --steps 5 --warmup 2 --no-pbr --no-cpu-baseline   # BOO only (counter runs)
+    python bench.py --steps 5 --warmup 2 --no-boo --no-cpu-baseline   # PBR only (counter runs)
 """
 
 from __future__ import annotations
@@ -250,6 +251,8 @@ def main():
                     help='BOO clustering (the headline workload is identity)')
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--no-pbr', action='store_true', help='skip the PBR line (profiling runs)')
+    ap.add_argument('--no-boo', action='store_true',
+                    help='skip BOO, so PBR is the measured path (PBR counter runs)')
     ap.add_argument('--calibrate-copy', action='store_true')
     ap.add_argument('--no-vendor', action='store_true', help='skip the rocSPARSE baseline')
     ap.add_argument('--no-cpp-timed', action='store_true',
@@ -286,7 +289,7 @@ def main():
     Ys = [torch.empty((1, m, K), device=dev) for _ in range(nrot)]
     stream = torch.cuda.current_stream().cuda_stream
     from oracle import oracle as O
-    has_boo = 'boo' in spec['formats']
+    has_boo = 'boo' in spec['formats'] and not args.no_boo
     run_pbr = 'pbr' in spec['formats'] and (not args.no_pbr or not has_boo)
     fmt = 'boo' if has_boo else 'pbr'
     ms_wall = ms_ev_mean = ms_api = ratio = None
@@ -312,10 +315,12 @@ def main():
             sys.exit(1)
         p_wall, p_ev = time_steps([lambda i=i: pbr_step(i) for i in range(nrot)], args.steps,
                                      args.warmup, torch)
+        pbr_workload = f'cfg{args.config}_{spec["name"]}_pbr8x8_thr{thr}_K{K}'
         pbr = {'ms_per_step': round(p_wall, 5), 'kernel_ms_mean': round(p_ev, 5),
                'gflops': round(flops / (p_wall * 1e-3) / 1e9, 2),
                'hbm_gbs': round(balg / (p_ev * 1e-3) / 1e9, 1),
-               'hbm_frac': round(balg / (p_ev * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+               'hbm_frac': round(balg / (p_ev * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+               'traffic': (traffic_from_profiles(pbr_workload) or {}).get('bytes_per_launch')}
         _log(f'PBR: wall {p_wall * 1e3:.1f} us/step, kernel {p_ev * 1e3:.1f} us')
         if not has_boo:                    # PBR is the measured path of this config
             ms_wall, ms_ev_mean, ratio = p_wall, p_ev, pratio
