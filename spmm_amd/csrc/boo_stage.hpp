@@ -69,6 +69,20 @@ constexpr int GATHER_CHUNK = 1024;
 // lengths the chunks' partial rows and fixup cost more than they save (48
 // entries per row: 248 -> 423 us at K=32), so the threshold stays as given.
 constexpr int GATHER_SKEWED_LONG = 32;
+// The gather pass walks its short rows in staging order, and rows next to
+// each other in that order run at about the same time on one XCD, so X rows
+// they share are fetched once into that XCD's L2.  When a Cuthill-McKee order
+// of the rows (breadth first over the rows their columns name) repeats more
+// of the X rows within a window of GATHER_REUSE_WINDOW rows than the slice
+// order does, by a factor of GATHER_REORDER_GAIN, the rows are walked in
+// that order instead.  Each row keeps its own entries and their order, so
+// its sum is the same; only which rows run side by side changes.  A randomly
+// permuted 27-point stencil (128^3, K=32) repeats 9.3x more X rows in that
+// order and its gather pass runs in 0.50 ms instead of 1.16 ms; an R-MAT
+// graph (2^20, K=128) repeats 1.32x more but runs 5.6 % slower (its row
+// order already keeps hub columns hot), hence a gain of 2 to switch.
+constexpr int GATHER_REUSE_WINDOW = 8192;
+constexpr double GATHER_REORDER_GAIN = 2.0;
 
 
 
@@ -374,6 +388,7 @@ private:
                 }
             }
         }
+        reorder_short_rows(S);
         S.n_crow_long = (int32_t)long_id.size();
         S.gtask_ptr.assign(1, 0);
         const int32_t base = (int32_t)S.ccol.size();
@@ -387,6 +402,84 @@ private:
             S.crow_ptr.push_back(base + long_ptr[i + 1]);
         }
         for (size_t e = 0; e < long_col.size(); ++e) put(S.ccol, S.cval, long_col[e], long_val[e]);
+    }
+
+    // Entries of the short gather rows, taken in `order`, whose column was
+    // named by a row at most GATHER_REUSE_WINDOW positions before (an X row
+    // another row nearby also reads).
+    long long window_reuse(const Staged& S, const std::vector<int32_t>& order) const {
+        std::vector<int32_t> last((size_t)in_.cols, -1);
+        long long hits = 0;
+        for (int32_t p = 0; p < (int32_t)order.size(); ++p) {
+            const int32_t i = order[p];
+            for (int32_t e = S.crow_ptr[i]; e < S.crow_ptr[i + 1]; ++e) {
+                const int32_t c = S.ccol[e];
+                if (last[c] >= 0 && p - last[c] <= GATHER_REUSE_WINDOW) ++hits;
+                last[c] = p;
+            }
+        }
+        return hits;
+    }
+
+    // Reorder the short gather rows (S.crow_id/crow_ptr/ccol/cval so far) by
+    // Cuthill-McKee when that repeats X rows within the window more often.
+    // Row i's neighbours are the short rows whose row id is one of its column
+    // ids (the matrix read as a graph; any order is correct, this one is
+    // local when the matrix is a graph with locality under some labelling).
+    void reorder_short_rows(Staged& S) {
+        const int32_t n = (int32_t)S.crow_id.size();
+        if (n < 2 || in_.rows != in_.cols) return;
+        std::vector<int32_t> pos_of_row((size_t)in_.rows, -1);
+        for (int32_t i = 0; i < n; ++i) pos_of_row[S.crow_id[i]] = i;
+        auto deg = [&](int32_t i) { return S.crow_ptr[i + 1] - S.crow_ptr[i]; };
+        // start nodes: unvisited rows by ascending length (ties: slice order)
+        std::vector<int32_t> starts(n);
+        for (int32_t i = 0; i < n; ++i) starts[i] = i;
+        std::stable_sort(starts.begin(), starts.end(), [&](int32_t a, int32_t b) { return deg(a) < deg(b); });
+        std::vector<int32_t> order;
+        order.reserve(n);
+        std::vector<char> seen(n, 0);
+        std::vector<int32_t> nb;
+        for (int32_t st : starts) {
+            if (seen[st]) continue;
+            seen[st] = 1;
+            size_t head = order.size();
+            order.push_back(st);
+            while (head < order.size()) {
+                const int32_t i = order[head++];
+                nb.clear();
+                for (int32_t e = S.crow_ptr[i]; e < S.crow_ptr[i + 1]; ++e) {
+                    const int32_t j = pos_of_row[S.ccol[e]];
+                    if (j >= 0 && !seen[j]) {
+                        seen[j] = 1;
+                        nb.push_back(j);
+                    }
+                }
+                std::stable_sort(nb.begin(), nb.end(), [&](int32_t a, int32_t b) { return deg(a) < deg(b); });
+                order.insert(order.end(), nb.begin(), nb.end());
+            }
+        }
+        std::vector<int32_t> ident(n);
+        for (int32_t i = 0; i < n; ++i) ident[i] = i;
+        const long long h0 = window_reuse(S, ident), h1 = window_reuse(S, order);
+        if ((double)h1 < GATHER_REORDER_GAIN * (double)h0 || h1 == h0) return;
+        std::vector<int32_t> rid, rptr(1, 0), col;
+        std::vector<char> val;
+        rid.reserve(n);
+        rptr.reserve((size_t)n + 1);
+        col.reserve(S.ccol.size());
+        val.reserve(S.cval.size());
+        for (int32_t i : order) {
+            rid.push_back(S.crow_id[i]);
+            col.insert(col.end(), S.ccol.begin() + S.crow_ptr[i], S.ccol.begin() + S.crow_ptr[i + 1]);
+            val.insert(val.end(), S.cval.begin() + (size_t)S.crow_ptr[i] * sizeof(T),
+                       S.cval.begin() + (size_t)S.crow_ptr[i + 1] * sizeof(T));
+            rptr.push_back((int32_t)col.size());
+        }
+        S.crow_id.swap(rid);
+        S.crow_ptr.swap(rptr);
+        S.ccol.swap(col);
+        S.cval.swap(val);
     }
 
     // Slices that share column chunks go into one group (up to G): a group

@@ -293,3 +293,44 @@ def test_gather_pass_skewed_rows_chunk_earlier():
     boo = S.csr_to_boo(E, cluster='identity', target_nr=32, target_nc=32)
     st = check_stream(E, boo, long_thr=256, min_reuse=1.5, group=4)
     assert len(st['crow_id']) == n and st['n_crow_long'] == 0
+
+
+def test_gather_rows_reordered_when_it_keeps_x_rows_close():
+    # A randomly permuted path graph (tridiagonal, 200,000 rows): in row order
+    # the rows naming any X row lie ~67,000 rows apart, beyond the staging's
+    # 8,192-row window; breadth-first order puts them next to each other, so
+    # the short gather rows are walked along the path: almost every row is a
+    # graph neighbour of the row before it.
+    n = 200_000
+    T = sp.diags([-np.ones(n - 1), 2 * np.ones(n), -np.ones(n - 1)], [-1, 0, 1], format='csr',
+                 dtype=np.float32)
+    p = np.random.default_rng(3).permutation(n)
+    A = T[p][:, p].tocsr()
+    st = _stage_sparse_checked(A)
+    cid = st['crow_id'][:len(st['crow_id']) - st['n_crow_long']]
+    assert len(cid) == n and not np.all(np.diff(cid) > 0)
+    Ac = A.tocoo()
+    edges = Ac.row.astype(np.int64) * n + Ac.col
+    adjacent = np.isin(cid[:-1].astype(np.int64) * n + cid[1:], edges)
+    assert adjacent.mean() > 0.99
+    # uniformly random columns: no order keeps X rows closer, row order stays
+    rng = np.random.default_rng(5)
+    R = sp.csr_matrix((rng.standard_normal(3 * n).astype(np.float32),
+                       (np.repeat(np.arange(n), 3), rng.integers(0, n, 3 * n))), shape=(n, n))
+    R.sum_duplicates()
+    st = _stage_sparse_checked(R)
+    cid = st['crow_id'][:len(st['crow_id']) - st['n_crow_long']]
+    assert len(cid) > 0.9 * n and np.all(np.diff(cid) > 0)
+
+
+def _stage_sparse_checked(A):
+    """Stage A (identity 32x32, the GPU path's knobs) and check, without
+    densifying, that the stream and gather pass hold A's values exactly."""
+    boo = S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32)
+    host = _host(boo)
+    st = _core.boo_stage(host, SB.MAX_ITEM_NNZ, SB.LONG_ROW_THRESHOLD, 4096, 4, SB.MIN_COL_REUSE)
+    r, c, v = decode(host, st)
+    B = sp.coo_matrix((v.astype(np.float64), (r, c)), shape=A.shape).tocsr()
+    assert B.nnz == A.nnz and abs(B - A.astype(np.float64)).max() == 0
+    assert np.array_equal(np.sort(st['crow_id']), np.unique(st['crow_id']))
+    return st
