@@ -111,6 +111,8 @@ typedef struct spmm_boo_stage spmm_boo_stage;  /* opaque, host memory */
 typedef struct spmm_boo_stage_info {
     int64_t n_tiles, n_ent, n_tcols, n_splits, n_long, n_crow, n_cnz, n_gtask;
     int32_t n_slots, n_waves, group, n_crow_long;
+    int32_t n_stream_rows;       /* rows the tile stream stores; n_stream_rows + n_crow == rows */
+    int64_t n_blob16;            /* record stream length in 16-byte units (0: none) */
 } spmm_boo_stage_info;
 
 /* group (1, 2 or 4): slices that share column chunks are put together, up to
@@ -143,12 +145,27 @@ int spmm_boo_stage_copy(const spmm_boo_stage* st, int32_t* tiles, uint16_t* tile
                         int32_t* long_rows, int32_t* wave_tiles, int32_t* crow_ptr,
                         int32_t* crow_id, int32_t* ccol, void* cval, int32_t* gtask,
                         int32_t* gtask_ptr);
+/* The record stream of a float matrix staged with group 4 (n_blob16 > 0): the
+ * same tiles as above, one contiguous 16-byte aligned record per wave and
+ * step (that step's entries, row starts, the ids of the X rows the wave
+ * stages and, at an item's end, the slice's row ids), so that the fastest
+ * kernel moves a whole step into LDS with one DMA instruction.
+ *   blobs [n_blob16*16] bytes, blob_first [n_waves*8] uint32 (per wave: the
+ *   offsets of its first 4 records, their sizes, its step count).
+ * Optional: a descriptor without it runs the same tiles through the other
+ * kernels (same results within the stated tolerance, slower). */
+int spmm_boo_stage_copy_blobs(const spmm_boo_stage* st, void* blobs, uint32_t* blob_first);
 void spmm_boo_stage_destroy(spmm_boo_stage* st);
 
 /* Device descriptor: the staged arrays plus row_ids and the remainder CSR
- * (read only for long_rows). */
+ * (read only for long_rows).  Every row of Y is stored either by the tile
+ * stream (n_stream_rows of them) or by the gather pass (n_crow), never both;
+ * spmm_boo_matmul returns SPMM_EINVAL unless n_stream_rows + n_crow == rows,
+ * so a descriptor that leaves either part unset cannot leave Y rows
+ * unwritten.  Copy both counts from spmm_boo_stage_info. */
 typedef struct spmm_boo_desc {
     int32_t rows, cols;
+    int32_t n_stream_rows;       /* rows stored by the tile stream (spmm_boo_stage_info) */
     const int32_t* row_ids;      /* [rows] */
     int32_t n_tiles;
     const int32_t* tiles;        /* [n_tiles*8] */
@@ -176,6 +193,9 @@ typedef struct spmm_boo_desc {
     const int32_t* rem_indptr;   /* [rows+1] */
     const int32_t* rem_col_ind;
     const void* rem_vals;
+    int64_t n_blob16;            /* record stream (spmm_boo_stage_copy_blobs); 0 and NULLs: none */
+    const void* blobs;           /* [n_blob16*16] bytes */
+    const uint32_t* blob_first;  /* [n_waves*8] */
 } spmm_boo_desc;
 
 /* Workspace bytes spmm_boo_matmul needs for this staging and shape: the

@@ -404,7 +404,11 @@ def spmm_reference(A: sp.csr_matrix, x: np.ndarray):
     """(Y64, B): the fp64 product of the original CSR with X, and the
     elementwise bound |A|.|X| that tolerances are stated against.  x may be
     [cols, K] or [batch, cols, K]."""
-    A64 = sp.csr_matrix(A, dtype=np.float64)
+    # A private copy: csr_matrix(A, dtype=...) shares A's index arrays, and
+    # scipy canonicalises a matrix in place (abs() sorts its indices), which
+    # would scramble a caller's matrix whose rows are not sorted.
+    A64 = sp.csr_matrix((np.asarray(A.data, dtype=np.float64), np.array(A.indices, copy=True),
+                         np.array(A.indptr, copy=True)), shape=A.shape)
     Aabs = abs(A64)
     x64 = np.asarray(x, dtype=np.float64)
     if x64.ndim == 2:

@@ -13,7 +13,7 @@ try:
 except ImportError as exc:  # pragma: no cover - exercised only on a broken install
     raise ImportError(
         'spmm_amd native extension is not built (spmm_amd/_core*.so, spmm_amd/libspmm_amd.so); '
-        'run `python -m spmm_amd.build` or `python -c "import __graft_entry__ as g; g.build()"`'
+        'run `python spmm_amd/build.py` or `python -c "import __graft_entry__ as g; g.build()"`'
     ) from exc
 
 __all__ = ['core']

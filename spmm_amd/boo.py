@@ -5,10 +5,12 @@ API and error behaviour follow ``torch_fast_spdmm/boo.py`` (reference):
 ``boo_matmul`` :230-354, ``boo_info`` / ``boo_arena_bytes`` :361-500.
 
 The arrays are produced by the native builder (``_core.csr_to_boo``), equal to
-the reference's ``csr_to_boo`` output.  On the GPU, ``boo_matmul`` runs the
-row-group kernel of ``libspmm_amd.so``: one wave per row group accumulates all
-of the group's blocks and its remainder rows in registers and stores each
-output row once, so there is no memset of Y and no atomic.
+the reference's ``csr_to_boo`` output.  ``.to('cuda')`` also stages them on the
+host into the kernels' schedule (``spmm_boo_stage_create``): 32-row slices cut
+into tiles of at most 32 columns, streamed by persistent workgroups that
+accumulate each slice in registers and store every output row once, plus a
+row-wise gather pass for empty slices and slices whose columns are too
+scattered to stage.  So there is no memset of Y and no atomic.
 """
 
 from __future__ import annotations
@@ -43,6 +45,7 @@ LONG_ROW_THRESHOLD = 256   # longer remainder rows go to the split-row pass
 WAVES_PER_CU = 16          # persistent waves per compute unit (4 per SIMD at <= 128 VGPRs)
 GROUP = 4                  # slices sharing X tiles per workgroup
 MIN_COL_REUSE = 1.5        # slices using each column less often go to the gather pass
+RECORD_STREAM = False      # hand the kernels the one-DMA-per-step record stream (boo_blob_kernel)
 
 
 class BooNzOrder(enum.IntEnum):
@@ -210,16 +213,19 @@ def _kernel_staging(rows, cols, d, rowmajor, row_ids_dev, device, rem_dev=None):
     }
     stage = core.boo_stage(host, MAX_ITEM_NNZ, LONG_ROW_THRESHOLD, max(GROUP, n_cu * WAVES_PER_CU), GROUP,
                            MIN_COL_REUSE)
-    g = types.SimpleNamespace(**{k: _pinned(stage[k], device) for k in (
-        'tiles', 'tile_rs', 'ent_val', 'ent_col', 'tcols', 'splits', 'long_rows',
-        'wave_tiles', 'crow_ptr', 'crow_id', 'ccol', 'cval', 'gtask', 'gtask_ptr')})
+    names = ['tiles', 'tile_rs', 'ent_val', 'ent_col', 'tcols', 'splits', 'long_rows',
+             'wave_tiles', 'crow_ptr', 'crow_id', 'ccol', 'cval', 'gtask', 'gtask_ptr']
+    records = RECORD_STREAM and int(stage['n_blob16']) > 0
+    if records:
+        names += ['blobs', 'blob_first']
+    g = types.SimpleNamespace(**{k: _pinned(stage[k], device) for k in names})
     if rem_dev is None:
         rem_dev = (_pinned(k_rem_indptr, device), _pinned(k_rem_col, device), _pinned(k_rem_val, device))
     torch.cuda.synchronize(device)
 
     p = lambda t: int(t.data_ptr())  # noqa: E731
     desc = {
-        'rows': rows, 'cols': cols, 'row_ids': p(row_ids_dev),
+        'rows': rows, 'cols': cols, 'n_stream_rows': int(stage['n_stream_rows']), 'row_ids': p(row_ids_dev),
         'n_tiles': int(stage['n_tiles']), 'tiles': p(g.tiles),
         'tile_rs': p(g.tile_rs), 'ent_val': p(g.ent_val), 'ent_col': p(g.ent_col),
         'tcols': p(g.tcols), 'n_waves': int(stage['n_waves']), 'group': int(stage['group']),
@@ -230,6 +236,8 @@ def _kernel_staging(rows, cols, d, rowmajor, row_ids_dev, device, rem_dev=None):
         'ccol': p(g.ccol), 'cval': p(g.cval), 'n_crow_long': int(stage['n_crow_long']),
         'n_gtask': int(stage['n_gtask']), 'gtask': p(g.gtask), 'gtask_ptr': p(g.gtask_ptr),
         'rem_indptr': p(rem_dev[0]), 'rem_col_ind': p(rem_dev[1]), 'rem_vals': p(rem_dev[2]),
+        'n_blob16': int(stage['n_blob16']) if records else 0,
+        'blobs': p(g.blobs) if records else 0, 'blob_first': p(g.blob_first) if records else 0,
     }
     return g, rem_dev, desc
 

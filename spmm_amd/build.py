@@ -8,7 +8,8 @@ Two artefacts, both next to this file:
   glue), compiled by g++ and linked against ``libspmm_amd.so`` through an
   ``$ORIGIN`` rpath.
 
-``python -m spmm_amd.build`` rebuilds both.  Nothing is JIT-compiled at import
+``python spmm_amd/build.py`` rebuilds both (run by path: importing the package
+needs the libraries this script builds).  Nothing is JIT-compiled at import
 time: ``spmm_amd`` loads what is here and fails loudly when it is missing.
 """
 

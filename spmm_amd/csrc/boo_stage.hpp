@@ -40,6 +40,7 @@
 #include <cstring>
 #include <stdexcept>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 namespace spmm_stage {
@@ -84,6 +85,27 @@ constexpr int GATHER_SKEWED_LONG = 32;
 constexpr int GATHER_REUSE_WINDOW = 8192;
 constexpr double GATHER_REORDER_GAIN = 2.0;
 
+// Blob stream (float, groups of 4): each wave's tiles again, one contiguous,
+// 16-byte aligned record per step, so that a wave moves a whole step's data
+// into LDS with one DMA instruction.  A record:
+//   word 0   nnz | nr << 8 | nc << 14 | flags << 20 | nvec(record 4 steps later) << 24
+//   word 1   slot (-1: the item stores Y)
+//   word 2   offset, in 16-byte units, of this wave's record 4 steps later
+//            (clamped to its last record)
+//   word 3   CONTIG: global id of the step's first X column (column c is
+//            id + min(c, nc - 1)); otherwise 0
+//   int32 cid[8]      (absent when CONTIG) X rows this wave stages in the step's
+//                     tile: entry j names column 2m + (j >> 2) + 8 (j & 3),
+//                     m = the wave's index in its workgroup, clamped to nc - 1
+//   uint8 rs[32]      (absent when nnz = 0) first entry of each row; row r
+//                     ends at rs[r + 1], row 31 at nnz
+//   int32 row_id[32]  (ROWIDS only) Y rows of the slice, for the store
+//   uint8 col[nnz]    local columns, then zero padding to 4 bytes
+//   float val[nnz]    then zero padding to 16 bytes
+constexpr uint32_t BLOB_LAST = 1u, BLOB_SERIAL = 2u, BLOB_ROWIDS = 4u, BLOB_CONTIG = 8u;
+constexpr int BLOB_MAX_BYTES = 16 + 32 + 32 + 128 + TILE_ENT + 4 * TILE_ENT;  // 848
+constexpr int BLOB_LOOKAHEAD = 4;
+
 
 
 struct Staged {
@@ -110,6 +132,13 @@ struct Staged {
     int32_t n_slots = 0;
     int32_t n_waves = 0;
     int32_t group = 1;               // waves per workgroup sharing X tiles
+    int32_t n_stream_rows = 0;       // rows the tile stream stores (the rest: crow_id)
+    // blob stream (float, group 4; empty otherwise): records in 16-byte units
+    // (4 words each), and per wave 8 words: offsets of its first 4 records
+    // (clamped to its last), their 16-byte counts packed one per byte, its
+    // step count, 0, 0
+    std::vector<uint32_t> blobs;
+    std::vector<uint32_t> blob_first;
     size_t n_tiles() const { return tiles.size() / TILE_WORDS; }
 };
 
@@ -150,13 +179,16 @@ public:
         S.tcols.assign(in_.col_ids, in_.col_ids + in_.cols);
         collect_slices(S);
         classify_slices();
-        for (const Slice& sl : slices_)  // long remainder rows of the tile stream's slices
-            if (!sl.csr)
-                for (size_t i = sl.g0; i < sl.g1; ++i) S.long_rows.push_back(longs_[i].row);
+        for (const Slice& sl : slices_) {  // long remainder rows of the tile stream's slices
+            if (sl.csr) continue;
+            S.n_stream_rows += sl.nr;
+            for (size_t i = sl.g0; i < sl.g1; ++i) S.long_rows.push_back(longs_[i].row);
+        }
         make_groups();
         for (size_t g = 0; g < groups_.size(); ++g) build_group_steps(S, g);
         split_heavy(S);
         deal_and_emit(S);
+        emit_blobs(S);
         emit_csr(S);
     }
 
@@ -193,7 +225,36 @@ private:
         int slot;       // -1: stores Y; else the partial slot of an item of a split slice
     };
 
+    // Every index the staging later uses to address a host array is checked
+    // here, so malformed input becomes invalid_argument (SPMM_EINVAL), never
+    // an out-of-range access: row groups, column ids and the remainder CSR.
+    void check_indices() const {
+        if (in_.row_grp_ptr[0] != 0 || in_.row_grp_ptr[in_.n_row_groups] != in_.rows)
+            throw std::invalid_argument("row_grp_ptr must run from 0 to rows");
+        if (in_.col_grp_ptr[0] != 0 || in_.col_grp_ptr[in_.n_col_groups] != in_.cols)
+            throw std::invalid_argument("col_grp_ptr must run from 0 to cols");
+        for (int g = 0; g < in_.n_col_groups; ++g)
+            if (in_.col_grp_ptr[g + 1] < in_.col_grp_ptr[g])
+                throw std::invalid_argument("col_grp_ptr is not nondecreasing");
+        for (int c = 0; c < in_.cols; ++c)
+            if (in_.col_ids[c] < 0 || in_.col_ids[c] >= in_.cols) throw std::invalid_argument("col_ids out of range");
+        if (in_.rem_indptr[0] != 0) throw std::invalid_argument("rem_indptr must start at 0");
+        for (int r = 0; r < in_.rows; ++r)
+            if (in_.rem_indptr[r + 1] < in_.rem_indptr[r])
+                throw std::invalid_argument("rem_indptr is not nondecreasing");
+        const int32_t n_rem = in_.rem_indptr[in_.rows];
+        if (n_rem > 0 && !in_.rem_col_ind) throw std::invalid_argument("rem_col_ind is null");
+        for (int32_t j = 0; j < n_rem; ++j)
+            if (in_.rem_col_ind[j] < 0 || in_.rem_col_ind[j] >= in_.cols)
+                throw std::invalid_argument("rem_col_ind out of range");
+        if (in_.num_blocks > 0 && in_.blk_nz_ptr[0] != 0) throw std::invalid_argument("blk_nz_ptr must start at 0");
+        for (int b = 0; b < in_.num_blocks; ++b)
+            if (in_.blk_nz_ptr[b + 1] < in_.blk_nz_ptr[b])
+                throw std::invalid_argument("blk_nz_ptr is not nondecreasing");
+    }
+
     void collect_slices(Staged& S) {
+        check_indices();
         int blk = 0;
         std::vector<Ent> ents;
         for (int rg = 0; rg < in_.n_row_groups; ++rg) {
@@ -826,6 +887,103 @@ private:
             }
         }
         finish(S);
+    }
+
+    // The blob stream, derived from the tile arrays just emitted (see the
+    // record layout above).  Only float matrices grouped by 4 get one; the
+    // kernels that read it need both.
+    void emit_blobs(Staged& S) {
+        S.blobs.clear();
+        S.blob_first.clear();
+        if (!std::is_same<T, float>::value || G_ != 4 || S.n_waves <= 0) return;
+        S.blob_first.assign((size_t)S.n_waves * 8, 0u);
+        std::vector<uint32_t> offs, nvec;
+        std::vector<uint8_t> rec;
+        for (int w = 0; w < S.n_waves; ++w) {
+            const int m = w % 4;
+            const int t0 = S.wave_tiles[w], t1 = S.wave_tiles[w + 1];
+            offs.clear();
+            nvec.clear();
+            for (int t = t0; t < t1; ++t) {
+                const int32_t* tw = &S.tiles[(size_t)t * TILE_WORDS];
+                const int ent_off = tw[0];
+                const uint32_t w1 = (uint32_t)tw[1];
+                const int nnz = (int)(w1 & 0xffu), nc = (int)((w1 >> 8) & 0xffu), nr = (int)((w1 >> 16) & 0xffu);
+                const uint32_t tflags = w1 >> 24;
+                const int cid_off = tw[2], row_off = tw[3], slot = tw[4];
+                uint32_t flags = 0;
+                if (tflags & FLAG_LAST) flags |= BLOB_LAST;
+                if (tflags & FLAG_SERIAL) flags |= BLOB_SERIAL;
+                const bool rowids = (tflags & FLAG_LAST) && slot < 0 && nr > 0;
+                if (rowids) flags |= BLOB_ROWIDS;
+                // X columns: contiguous ids need only the first
+                bool contig = true;
+                int ncx = nc;
+                int32_t base = 0;
+                if (nc == 0) {
+                    ncx = 1;          // nothing to stage: load X row 0, never read
+                } else {
+                    base = S.tcols[(size_t)cid_off];
+                    for (int c = 1; c < nc && contig; ++c) contig = S.tcols[(size_t)cid_off + c] == base + c;
+                }
+                if (contig) flags |= BLOB_CONTIG;
+                rec.clear();
+                auto put32 = [&](uint32_t v) {
+                    for (int k = 0; k < 4; ++k) rec.push_back((uint8_t)(v >> (8 * k)));
+                };
+                put32((uint32_t)nnz | (uint32_t)nr << 8 | (uint32_t)ncx << 14 | flags << 20);
+                put32((uint32_t)slot);
+                put32(0u);            // patched below
+                put32(contig ? (uint32_t)base : 0u);
+                if (!contig)
+                    for (int j = 0; j < 8; ++j) {
+                        const int c = std::min(2 * m + (j >> 2) + 8 * (j & 3), nc - 1);
+                        put32((uint32_t)S.tcols[(size_t)cid_off + c]);
+                    }
+                if (nnz > 0)
+                    for (int r = 0; r < TILE_ROWS; ++r) {
+                        const uint16_t v = S.tile_rs[(size_t)t * TILE_RS + r];
+                        if (v > 255) throw std::invalid_argument("tile row start exceeds a byte");
+                        rec.push_back((uint8_t)v);
+                    }
+                if (rowids)
+                    for (int r = 0; r < TILE_ROWS; ++r) put32(r < nr ? (uint32_t)in_.row_ids[row_off + r] : 0u);
+                for (int e = 0; e < nnz; ++e) rec.push_back(S.ent_col[(size_t)ent_off + e]);
+                while (rec.size() & 3) rec.push_back(0);
+                const size_t vbytes = (size_t)nnz * sizeof(T);
+                const char* vp = S.ent_val.data() + (size_t)ent_off * sizeof(T);
+                rec.insert(rec.end(), vp, vp + vbytes);
+                while (rec.size() & 15) rec.push_back(0);
+                if ((int)rec.size() > BLOB_MAX_BYTES) throw std::invalid_argument("blob record too large");
+                offs.push_back((uint32_t)(S.blobs.size() / 4));
+                nvec.push_back((uint32_t)(rec.size() / 16));
+                const size_t at = S.blobs.size();
+                S.blobs.resize(at + rec.size() / 4);
+                std::memcpy(&S.blobs[at], rec.data(), rec.size());
+            }
+            const int n = t1 - t0;
+            for (int k = 0; k < n; ++k) {
+                const int nx = std::min(k + BLOB_LOOKAHEAD, n - 1);
+                uint32_t* hw = &S.blobs[(size_t)offs[k] * 4];
+                hw[0] |= nvec[nx] << 24;
+                hw[2] = offs[nx];
+            }
+            uint32_t* f = &S.blob_first[(size_t)w * 8];
+            if (n > 0) {
+                uint32_t packed = 0;
+                for (int k = 0; k < BLOB_LOOKAHEAD; ++k) {
+                    const int kk = std::min(k, n - 1);
+                    f[k] = offs[kk];
+                    packed |= nvec[kk] << (8 * k);
+                }
+                f[4] = packed;
+            }
+            f[5] = (uint32_t)n;
+        }
+        if (S.blobs.size() / 4 + 64 >= (size_t)1 << 28) {   // 4 GiB: DMA offsets are 32-bit bytes
+            S.blobs.clear();
+            S.blob_first.clear();
+        }
     }
 
     void finish(Staged& S) {

@@ -271,6 +271,7 @@ spmm_boo_desc boo_desc(const py::dict& d) {
     spmm_boo_desc A{};
     A.rows = d["rows"].cast<int32_t>();
     A.cols = d["cols"].cast<int32_t>();
+    A.n_stream_rows = d["n_stream_rows"].cast<int32_t>();
     A.row_ids = reinterpret_cast<const int32_t*>(P(d, "row_ids"));
     A.n_tiles = d["n_tiles"].cast<int32_t>();
     A.tiles = reinterpret_cast<const int32_t*>(P(d, "tiles"));
@@ -298,6 +299,11 @@ spmm_boo_desc boo_desc(const py::dict& d) {
     A.rem_indptr = reinterpret_cast<const int32_t*>(P(d, "rem_indptr"));
     A.rem_col_ind = reinterpret_cast<const int32_t*>(P(d, "rem_col_ind"));
     A.rem_vals = reinterpret_cast<const void*>(P(d, "rem_vals"));
+    if (d.contains("n_blob16")) {
+        A.n_blob16 = d["n_blob16"].cast<int64_t>();
+        A.blobs = reinterpret_cast<const void*>(P(d, "blobs"));
+        A.blob_first = reinterpret_cast<const uint32_t*>(P(d, "blob_first"));
+    }
     return A;
 }
 
@@ -349,9 +355,15 @@ py::dict boo_stage(const py::dict& h, int32_t max_item_nnz, int32_t long_thresho
                                        ecol.data(), tcols.data(), splits.data(), longr.data(), wt.data(),
                                        crp.data(), cri.data(), ccol.data(),
                                        inf.n_cnz ? cv.mutable_data() : nullptr, gt.data(), gtp.data());
+    std::vector<uint32_t> blobs((size_t)inf.n_blob16 * 4), bfirst(inf.n_blob16 > 0 ? (size_t)inf.n_waves * 8 : 0);
+    const int rc2 = rc ? rc : spmm_boo_stage_copy_blobs(st, blobs.data(), bfirst.data());
     spmm_boo_stage_destroy(st);
     raise_status(rc);
+    raise_status(rc2);
     py::dict d;
+    d["blobs"] = give(std::move(blobs));
+    d["blob_first"] = give(std::move(bfirst));
+    d["n_blob16"] = inf.n_blob16;
     d["tiles"] = give(std::move(tiles));
     d["tile_rs"] = give(std::move(rs));
     d["ent_val"] = ev;
@@ -368,6 +380,7 @@ py::dict boo_stage(const py::dict& h, int32_t max_item_nnz, int32_t long_thresho
     d["gtask"] = give(std::move(gt));
     d["gtask_ptr"] = give(std::move(gtp));
     d["n_crow_long"] = inf.n_crow_long;
+    d["n_stream_rows"] = inf.n_stream_rows;
     d["n_gtask"] = inf.n_gtask;
     d["n_tiles"] = inf.n_tiles;
     d["n_slots"] = inf.n_slots;

@@ -161,6 +161,8 @@ struct StreamArgs {
     const T* X;
     T* Y;
     T* P;
+    const uint32_t* blobs;       // record stream (float, group 4), or null
+    const uint32_t* blob_first;
 };
 
 // &Xb[row*K + f].  A32: the X slab of one batch is under 4 GiB, so the byte
@@ -799,6 +801,271 @@ __global__ void __launch_bounds__(256, 4) boo_stream_dma_kernel(StreamArgs<float
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
+// ---------------------------------------------------------------------------
+// BOO tile stream, float, 64-feature tiles, every load a DMA into LDS.
+//
+// The same groups and lock step as boo_stream_dma_kernel, but a wave's whole
+// share of a step -- entries, row starts, the ids of the X rows it stages and,
+// at an item's end, the slice's row ids -- is one contiguous record of the
+// blob stream (boo_stage.hpp), moved into LDS by a single
+// global_load_lds_dwordx4 BLOB_LOOKAHEAD = 4 steps ahead; the step's X tile
+// is moved DX steps ahead into a ring of DX + 1 tiles.  No load lands in a
+// register, so every wait is explicit and counted: at the top of step t a
+// wave needs what it issued two steps earlier (DX = 2: its share of X tile
+// t, and record t + 2 whose column ids name the X rows of tile t + 2) and
+// lets the later step's X share, stores and record stay in flight.  Y rows
+// are written by inline-asm stores so that their count is known exactly.
+// Per step a wave issues: its 2 X DMA instructions (top), at an item's end
+// 8 stores, then the DMA of record t + 4 into the buffer record t used
+// (bottom).
+// ---------------------------------------------------------------------------
+
+constexpr int BLOB_BUF = 864;   // LDS bytes per record buffer (>= the largest record + read-ahead)
+constexpr uint32_t BL_LAST = 1u, BL_SERIAL = 2u, BL_ROWIDS = 4u, BL_CONTIG = 8u;
+
+template <int DX>
+struct StBlobLds {
+    float xt[DX + 1][8 * DMA_BLK / 4];    // X tile ring
+    float syn[8 * DMA_BLK / 4];            // serial rows: wave w's are columns 8w .. 8w+7
+    uint8_t rec[4][4][BLOB_BUF];           // [wave][step mod 4] record buffers
+};
+
+struct BlobArgs {
+    int rows, cols, K, batch, n_waves;
+    const uint32_t* blobs;   // records, 16-byte units
+    const uint32_t* first;   // [n_waves][8]
+    const float* X;
+    float* Y;
+    float* P;
+};
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+// 8 x 16-byte stores of one lane's 32 features (chunks 32 bytes apart).
+__device__ __forceinline__ void store8(float* p, const f4_t (&d)[8]) {
+    asm volatile(
+        "global_store_dwordx4 %0, %1, off\n\t"
+        "global_store_dwordx4 %0, %2, off offset:32\n\t"
+        "global_store_dwordx4 %0, %3, off offset:64\n\t"
+        "global_store_dwordx4 %0, %4, off offset:96\n\t"
+        "global_store_dwordx4 %0, %5, off offset:128\n\t"
+        "global_store_dwordx4 %0, %6, off offset:160\n\t"
+        "global_store_dwordx4 %0, %7, off offset:192\n\t"
+        "global_store_dwordx4 %0, %8, off offset:224" ::"v"(p),
+        "v"(d[0]), "v"(d[1]), "v"(d[2]), "v"(d[3]), "v"(d[4]), "v"(d[5]), "v"(d[6]), "v"(d[7])
+        : "memory");
+}
+
+template <int DX>
+__global__ void __launch_bounds__(256, DX >= 2 ? 3 : 4) boo_blob_kernel(BlobArgs a, int kt0) {
+    static_assert(DX == 1 || DX == 2, "X tiles are staged 1 or 2 steps ahead");
+    __shared__ __attribute__((aligned(16))) StBlobLds<DX> L;
+    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int w = xcd_remap(blockIdx.x, gridDim.x) * 4 + wv;
+    if (w >= a.n_waves) return;  // uniform per workgroup: n_waves is a multiple of 4
+    // the wave's 8 words, held in SGPRs before any DMA: a vector load here
+    // would enter the counted waits below
+    const uint32_t* F = a.first + 8 * (size_t)w;
+    uint32_t fw[6];
+#pragma unroll
+    for (int k = 0; k < 6; ++k) fw[k] = (uint32_t)__builtin_amdgcn_readfirstlane((int)F[k]);
+    asm volatile("" ::"s"(fw[0]), "s"(fw[1]), "s"(fw[2]), "s"(fw[3]), "s"(fw[4]), "s"(fw[5]));
+    const int nsteps = (int)fw[5];
+    if (nsteps <= 0) return;     // uniform per workgroup: its streams have equal lengths
+    const int lane = threadIdx.x & 63;
+    const int h = lane & 1;
+    const int lr = lane >> 1;
+    const int fbase = (kt0 + (int)blockIdx.y) * 64;
+    const int b = blockIdx.z;
+    const int K = a.K;
+    const float* Xb = a.X + (size_t)b * a.cols * K;
+    const uint32_t rowb = (uint32_t)K * 4u;
+    const uint32_t lane_x = (uint32_t)fbase * 4u + (uint32_t)(lane & 15) * 16u;
+    const int kq = lane >> 4;  // column I + 8 kq of DMA instruction I
+    const uint32_t x_lds = lds_u32(&L.xt[0][0]);
+
+    auto rec_ptr = [&](int n) { return &L.rec[wv][n & 3][0]; };
+    auto issue_rec = [&](uint32_t off16, uint32_t nvec, int n) {
+        if ((uint32_t)lane < nvec)
+            dma16(reinterpret_cast<const float*>(a.blobs), off16 * 16u + (uint32_t)lane * 16u,
+                  (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_u32(rec_ptr(n))));
+    };
+    // this wave's two DMA instructions (2 wv, 2 wv + 1) of X tile n, whose
+    // column ids are in record n
+    auto issue_x = [&](int n) {
+        const uint8_t* rp = rec_ptr(n);
+        const uint32_t w0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)*reinterpret_cast<const uint32_t*>(rp));
+        const uint32_t nc = (w0 >> 14) & 63u;
+        uint32_t id0, id1;
+        if ((w0 >> 20) & BL_CONTIG) {
+            const uint32_t base =
+                (uint32_t)__builtin_amdgcn_readfirstlane((int)*reinterpret_cast<const uint32_t*>(rp + 12));
+            const uint32_t c0 = (uint32_t)(2 * wv + 8 * kq);
+            id0 = base + min(c0, nc - 1u);
+            id1 = base + min(c0 + 1u, nc - 1u);
+        } else {
+            const uint32_t* cid = reinterpret_cast<const uint32_t*>(rp + 16);
+            id0 = cid[kq];
+            id1 = cid[4 + kq];
+        }
+        const uint32_t l0 = x_lds + (uint32_t)(n % (DX + 1)) * (8u * DMA_BLK) + (uint32_t)(2 * wv) * DMA_BLK;
+        dma16(Xb, __umul24(id0, rowb) + lane_x, l0);
+        dma16(Xb, __umul24(id1, rowb) + lane_x, l0 + (uint32_t)DMA_BLK);
+    };
+
+    // prologue: the last operations before step 0 are laid out as the steady
+    // state leaves them, so step 0 waits like any other step
+    {
+        const uint32_t nv = fw[4];
+        if constexpr (DX == 2) {
+            issue_rec(fw[0], nv & 0xffu, 0);
+            issue_rec(fw[1], (nv >> 8) & 0xffu, 1);
+            wait_vm<1>();                       // record 0
+            issue_x(0);
+            issue_rec(fw[2], (nv >> 16) & 0xffu, 2);
+            wait_vm<3>();                       // record 1
+            issue_x(1);
+            issue_rec(fw[3], nv >> 24, 3);
+        } else {
+            issue_rec(fw[0], nv & 0xffu, 0);
+            issue_rec(fw[1], (nv >> 8) & 0xffu, 1);
+            issue_rec(fw[2], (nv >> 16) & 0xffu, 2);
+            wait_vm<2>();                       // record 0
+            issue_x(0);
+            issue_rec(fw[3], nv >> 24, 3);
+        }
+    }
+
+    f4_t acc[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) acc[q] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+    typedef __attribute__((address_space(3))) const char lds_char;
+    bool stored_prev = false;
+    for (int n = 0; n < nsteps; ++n) {
+        // (1) X tile n (every wave's share) and record n + DX (own) are in
+        // LDS; the barrier publishes the tile
+        if constexpr (DX == 2) {
+            if (stored_prev) asm volatile("s_waitcnt vmcnt(11) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            else asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        } else {
+            if (stored_prev) asm volatile("s_waitcnt vmcnt(9) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            else asm volatile("s_waitcnt vmcnt(1) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // (2) X tile n + DX into the buffer tile n - 1 used
+        issue_x(n + DX);
+        __builtin_amdgcn_sched_barrier(0);
+        // (3) record n
+        const uint8_t* rp = rec_ptr(n);
+        const uint32_t w0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)*reinterpret_cast<const uint32_t*>(rp));
+        const int slot = __builtin_amdgcn_readfirstlane((int)*reinterpret_cast<const uint32_t*>(rp + 4));
+        const uint32_t next_off =
+            (uint32_t)__builtin_amdgcn_readfirstlane((int)*reinterpret_cast<const uint32_t*>(rp + 8));
+        const int nnz = (int)(w0 & 0xffu);
+        const int nr = (int)((w0 >> 8) & 63u);
+        const uint32_t fl = (w0 >> 20) & 15u;
+        const uint32_t next_nvec = w0 >> 24;
+        int p = 16 + ((fl & BL_CONTIG) ? 0 : 32);
+        const int p_rs = p;
+        p += nnz > 0 ? 32 : 0;
+        const int p_rid = p;
+        p += (fl & BL_ROWIDS) ? 128 : 0;
+        const uint8_t* cols = rp + p;
+        const float* vals = reinterpret_cast<const float*>(rp + p + ((nnz + 3) & ~3));
+        int rs0 = 0, rs1 = 0;
+        if (nnz > 0) {
+            rs0 = rp[p_rs + lr];
+            rs1 = lr == ST_ROWS - 1 ? nnz : (int)rp[p_rs + lr + 1];
+        }
+        const float* tile = &L.xt[n % (DX + 1)][0];
+        // (4) the walk
+        if (fl & BL_SERIAL) {
+            // few busy rows: the whole wave takes one busy row at a time,
+            // lane f on feature f, and leaves its sums in syn for the row's lanes
+            uint64_t busy = __ballot(h == 0 && rs0 != rs1);
+            int mine = -1;
+            const char* xc = reinterpret_cast<const char*>(tile) + lane * 4;
+            for (int k = 0; busy; ++k) {
+                const int l2 = __builtin_ctzll(busy);
+                busy &= busy - 1;
+                int j = __builtin_amdgcn_readlane(rs0, l2);
+                const int e = __builtin_amdgcn_readlane(rs1, l2);
+                float s0 = 0.f, s1 = 0.f;
+                for (; j + 2 <= e; j += 2) {
+                    const uint32_t c0 = cols[j], c1 = cols[j + 1];
+                    s0 += vals[j] * *reinterpret_cast<const float*>(xc + dma_col_off(c0));
+                    s1 += vals[j + 1] * *reinterpret_cast<const float*>(xc + dma_col_off(c1));
+                }
+                if (j < e) s0 += vals[j] * *reinterpret_cast<const float*>(xc + dma_col_off(cols[j]));
+                *reinterpret_cast<float*>(reinterpret_cast<char*>(L.syn) + dma_col_off(8 * wv + k) + lane * 4) =
+                    s0 + s1;
+                if ((lane & ~1) == l2) mine = k;
+            }
+            wave_lds_fence();
+            if (mine >= 0) {
+                lds_char* sr = (lds_char*)(L.syn) + dma_col_off(8 * wv + mine) + h * 16;
+                const f4_t* xr = (const f4_t*)sr;
+                f4_t x[8];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) x[q] = xr[2 * q];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) acc[q] += x[q];
+            }
+        } else if (rs0 < rs1) {
+            lds_char* tb = (lds_char*)(tile) + h * 16;
+            int j = rs0;
+            uint32_t c = cols[j];
+            float v = vals[j];
+#pragma nounroll
+            for (; j < rs1; ++j) {
+                const uint32_t cn = cols[j + 1];
+                const float vn = vals[j + 1];
+                __builtin_amdgcn_sched_barrier(0);
+                const f4_t* xr = (const f4_t*)(lds_char*)(tb + dma_col_off(c));
+                f4_t x[8];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) x[q] = xr[2 * q];
+                const f4_t vv = f4_t{v, v, v, v};
+#pragma unroll
+                for (int q = 0; q < 8; ++q) acc[q] = __builtin_elementwise_fma(vv, x[q], acc[q]);
+                c = cn;
+                v = vn;
+            }
+        }
+        wave_lds_fence();
+        // (5) end of the item: store its rows
+        stored_prev = false;
+        if ((fl & BL_LAST) && nr > 0) {
+            if (lr < nr) {
+                float* out;
+                if (slot < 0) {
+                    const int row = *reinterpret_cast<const int*>(rp + p_rid + 4 * lr);
+                    out = a.Y + ((size_t)b * a.rows + row) * K + fbase + h * 4;
+                } else {
+                    out = a.P + (((size_t)slot * a.batch + b) * ST_ROWS + lr) * K + fbase + h * 4;
+                }
+                store8(out, acc);
+            }
+#pragma unroll
+            for (int q = 0; q < 8; ++q) acc[q] = f4_t{0.f, 0.f, 0.f, 0.f};
+            stored_prev = true;
+        }
+        // (6) record n + 4 into this record's buffer, once its reads are done
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        issue_rec(next_off, next_nvec, n);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // the last DMAs land before the workgroup's LDS is released
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
 template <typename T>
 __global__ void __launch_bounds__(256) fill_zero_kernel(T* __restrict__ Y, size_t n) {
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) Y[i] = T(0);
@@ -1302,6 +1569,9 @@ int boo_pick_f(int K) {
 #ifndef SPMM_BOO_FAR
 #define SPMM_BOO_FAR 2          // streaming tile data loaded this many tiles ahead
 #endif
+#ifndef SPMM_BOO_BLOB_DX
+#define SPMM_BOO_BLOB_DX 2      // X tiles of the record-stream kernel staged this many steps ahead
+#endif
 
 // Full feature tiles in one launch, a partial last tile (K % 2F != 0) in a
 // second one compiled with the per-chunk feature guards.
@@ -1320,6 +1590,14 @@ int launch_boo_stream_a(const StreamArgs<T>& a, hipStream_t s) {
         return check_launch("boo_stream_kernel");
     };
     if constexpr (std::is_same<T, float>::value && F == 32 && VEC == 4 && A32) {
+        if (wg4 && full > 0 && a.blobs && a.blob_first) {  // full 64-feature tiles, every load a DMA
+            const dim3 grid(round_up8(a.n_waves / 4), full, a.batch);
+            BlobArgs ba{a.rows, a.cols, a.K, a.batch, a.n_waves, a.blobs, a.blob_first, a.X, a.Y, a.P};
+            hipLaunchKernelGGL((boo_blob_kernel<SPMM_BOO_BLOB_DX>), grid, dim3(256), 0, s, ba, 0);
+            const int rc = check_launch("boo_blob_kernel");
+            if (rc || a.K % (2 * F) == 0) return rc;
+            return go(boo_stream_kernel<T, F, VEC, D, DF, 4, false, A32>, 4, 1, full);
+        }
         if (wg4 && full > 0) {  // full 64-feature tiles: X staged by LDS DMA
             const dim3 grid(round_up8(a.n_waves / 4), full, a.batch);
             hipLaunchKernelGGL((boo_stream_dma_kernel<DF>), grid, dim3(256), 0, s, a, 0);
@@ -1451,6 +1729,15 @@ int boo_matmul_t(const spmm_boo_desc* A, const void* Xv, void* Yv, int64_t batch
                  void* ws, size_t ws_bytes, hipStream_t s) {
     const T* X = static_cast<const T*>(Xv);
     T* Y = static_cast<T*>(Yv);
+    // Y rows come from the tile stream or the gather pass; a descriptor whose
+    // counts do not add up to rows would leave rows of Y unwritten.
+    if (A->n_stream_rows < 0 || A->n_crow < 0 || (long long)A->n_stream_rows + A->n_crow != A->rows)
+        return fail(SPMM_EINVAL,
+                    "BOO descriptor covers %d tile-stream rows + %d gather rows, not the matrix's %d rows; "
+                    "copy n_stream_rows, n_crow and every gather-pass array from the staging",
+                    A->n_stream_rows, A->n_crow, A->rows);
+    if (A->n_stream_rows > 0 && A->n_tiles <= 0)
+        return fail(SPMM_EINVAL, "BOO descriptor has %d tile-stream rows but no tiles", A->n_stream_rows);
     if (A->rows == 0 || K == 0 || batch == 0) return SPMM_OK;
     const bool stream = A->n_tiles > 0;
     if ((!stream && A->n_crow <= 0) || (stream && (A->n_waves <= 0 || !A->wave_tiles || !A->tiles)))
@@ -1491,6 +1778,9 @@ int boo_matmul_t(const spmm_boo_desc* A, const void* Xv, void* Yv, int64_t batch
     a.X = X;
     a.Y = Y;
     a.P = static_cast<T*>(ws);
+    const bool recs = A->n_blob16 > 0 && A->blobs && A->blob_first;
+    a.blobs = recs ? static_cast<const uint32_t*>(A->blobs) : nullptr;
+    a.blob_first = recs ? A->blob_first : nullptr;
     int rc = stream ? boo_dispatch<T>(a, s) : SPMM_OK;
     if (rc) return rc;
     if (A->n_crow > 0) {
@@ -1667,6 +1957,8 @@ int spmm_boo_stage_sizes(const spmm_boo_stage* st, spmm_boo_stage_info* info) {
     info->n_crow = (int64_t)st->s.crow_id.size();
     info->n_cnz = (int64_t)st->s.ccol.size();
     info->n_crow_long = st->s.n_crow_long;
+    info->n_stream_rows = st->s.n_stream_rows;
+    info->n_blob16 = (int64_t)(st->s.blobs.size() / 4);
     info->n_gtask = (int64_t)(st->s.gtask.size() / 2);
     info->n_slots = st->s.n_slots;
     info->n_waves = st->s.n_waves;
@@ -1699,6 +1991,16 @@ int spmm_boo_stage_copy(const spmm_boo_stage* st, int32_t* tiles, uint16_t* tile
               put(gtask, s.gtask.data(), s.gtask.size() * 4) &&
               put(gtask_ptr, s.gtask_ptr.data(), s.gtask_ptr.size() * 4);
     return ok ? SPMM_OK : fail(SPMM_EINVAL, "null output array for a non-empty staging field");
+}
+
+int spmm_boo_stage_copy_blobs(const spmm_boo_stage* st, void* blobs, uint32_t* blob_first) {
+    if (!st) return fail(SPMM_EINVAL, "null staging handle");
+    const spmm_stage::Staged& s = st->s;
+    if (s.blobs.empty()) return SPMM_OK;
+    if (!blobs || !blob_first) return fail(SPMM_EINVAL, "null output array for the record stream");
+    std::memcpy(blobs, s.blobs.data(), s.blobs.size() * 4);
+    std::memcpy(blob_first, s.blob_first.data(), s.blob_first.size() * 4);
+    return SPMM_OK;
 }
 
 void spmm_boo_stage_destroy(spmm_boo_stage* st) { delete st; }

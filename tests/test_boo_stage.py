@@ -334,3 +334,157 @@ def _stage_sparse_checked(A):
     assert B.nnz == A.nnz and abs(B - A.astype(np.float64)).max() == 0
     assert np.array_equal(np.sort(st['crow_id']), np.unique(st['crow_id']))
     return st
+
+
+# ---------------------------------------------------------------------------
+# record stream (float, group 4): one DMA-able record per wave and step
+# ---------------------------------------------------------------------------
+
+def decode_records(st):
+    """Walk each wave's records by their own look-ahead links (records 0-3
+    from the wave's first words, record k >= 4 from record k - 4's link) and
+    return, per wave, the decoded records (dicts).  Independent of the
+    kernel: follows the byte layout the staging documents."""
+    blobs = st['blobs'].view(np.uint8)
+    first = st['blob_first'].reshape(-1, 8)
+    out = []
+    for w in range(st['n_waves']):
+        f = first[w]
+        recs = []
+        for k in range(int(f[5])):
+            if k < 4:
+                o, nv = int(f[k]), (int(f[4]) >> (8 * k)) & 0xff
+            else:
+                o, nv = recs[k - 4]['next_off'], recs[k - 4]['next_nvec']
+            rec = blobs[o * 16:(o + nv) * 16]
+            h = rec[:16].view(np.uint32)
+            w0 = int(h[0])
+            d = {'nnz': w0 & 0xff, 'nr': (w0 >> 8) & 63, 'nc': (w0 >> 14) & 63, 'flags': (w0 >> 20) & 15,
+                 'slot': int(np.int32(h[1])), 'next_off': int(h[2]), 'next_nvec': w0 >> 24,
+                 'base': int(h[3]), 'off': o, 'nvec': nv}
+            p = 16
+            if not d['flags'] & 8:
+                d['cid'] = rec[p:p + 32].view(np.int32).copy()
+                p += 32
+            if d['nnz']:
+                d['rs'] = rec[p:p + 32].copy()
+                p += 32
+            if d['flags'] & 4:
+                d['rowid'] = rec[p:p + 128].view(np.int32).copy()
+                p += 128
+            nnz = d['nnz']
+            d['col'] = rec[p:p + nnz].copy()
+            p += (nnz + 3) & ~3
+            d['val'] = rec[p:p + 4 * nnz].view(np.float32).copy()
+            p += 4 * nnz
+            assert (p + 15) // 16 == nv          # the record is exactly its 16-byte count
+            recs.append(d)
+        out.append(recs)
+    return out
+
+
+@pytest.mark.parametrize('case', ['stencil', 'permuted', 'rmat', 'heavy'])
+def test_record_stream_matches_tiles(case):
+    """The record stream holds exactly the tiles of the tile stream: per wave
+    and step its entries, row starts, the X rows it stages (2 of the 8 DMA
+    instructions of the step's 32-column tile), the slice's row ids at an
+    item's end; each record's look-ahead link names the record 4 steps later
+    (the last one for the stream's final records)."""
+    if case == 'stencil':
+        A = M.stencil_27pt(16)
+    elif case == 'permuted':
+        A = M.permuted(M.stencil_27pt(12), seed=3)
+    elif case == 'rmat':
+        A = M.rmat(12, 8, seed=1)
+    else:   # heavy slices: split items with partial slots
+        rng = np.random.default_rng(5)
+        A = sp.random(96, 96, density=0.9, random_state=rng, format='csr', dtype=np.float32)
+    A = sp.csr_matrix(A, dtype=np.float32)
+    boo = S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32)
+    host = _host(boo)
+    st = _core.boo_stage(host, 512 if case == 'heavy' else 4096, 256, 64, 4, 1.5)
+    if st['n_waves'] == 0:
+        assert st['n_blob16'] == 0
+        return
+    assert st['n_blob16'] == len(st['blobs']) // 4 > 0
+    tiles = st['tiles'].reshape(-1, 8)
+    trs = st['tile_rs'].reshape(-1, 33)
+    wt = st['wave_tiles']
+    recs = decode_records(st)
+    for w in range(st['n_waves']):
+        m = w % 4
+        t0, t1 = wt[w], wt[w + 1]
+        assert len(recs[w]) == t1 - t0
+        for k, t in enumerate(range(t0, t1)):
+            d = recs[w][k]
+            eo, w1, co, ro, slot = (int(x) for x in tiles[t][:5])
+            nnz, nc, nr, fl = w1 & 0xff, (w1 >> 8) & 0xff, (w1 >> 16) & 0xff, (w1 >> 24) & 0xff
+            assert (d['nnz'], d['nr'], d['slot']) == (nnz, nr, slot)
+            assert d['flags'] & 1 == fl & 1 and (d['flags'] >> 1) & 1 == (fl >> 1) & 1
+            if nnz:
+                assert np.array_equal(d['rs'].astype(int), trs[t][:32].astype(int))
+            assert np.array_equal(d['col'], st['ent_col'][eo:eo + nnz])
+            assert np.array_equal(d['val'], st['ent_val'][eo:eo + nnz])
+            # the X rows this wave stages: column 2m + (j >> 2) + 8 (j & 3)
+            cols = [min(2 * m + (j >> 2) + 8 * (j & 3), max(nc - 1, 0)) for j in range(8)]
+            want = [st['tcols'][co + c] if nc else 0 for c in cols]
+            if d['flags'] & 8:
+                got = [d['base'] + min(2 * m + (j >> 2) + 8 * (j & 3), d['nc'] - 1) for j in range(8)]
+            else:
+                got = list(d['cid'])
+            assert got == want
+            if (fl & 1) and slot < 0 and nr > 0:
+                assert d['flags'] & 4
+                assert np.array_equal(d['rowid'][:nr], host['row_ids'][ro:ro + nr])
+            else:
+                assert not d['flags'] & 4
+    # the 4-step links: past the stream's end they name its last record (the
+    # kernel prefetches it again and never uses it); every record lies inside
+    # the stream
+    blobs16 = len(st['blobs']) // 4
+    first = st['blob_first'].reshape(-1, 8)
+    for w in range(st['n_waves']):
+        n = len(recs[w])
+        for k in range(n):
+            assert recs[w][k]['off'] + recs[w][k]['nvec'] <= blobs16
+            nx = recs[w][min(k + 4, n - 1)]
+            assert (recs[w][k]['next_off'], recs[w][k]['next_nvec']) == (nx['off'], nx['nvec'])
+        for k in range(4):
+            assert int(first[w][k]) == recs[w][min(k, n - 1)]['off']
+
+
+def test_record_stream_absent_for_double_and_small_groups():
+    A = sp.csr_matrix(M.stencil_27pt(8), dtype=np.float64)
+    boo = S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32)
+    st = _core.boo_stage(_host(boo), 4096, 256, 64, 4, 1.5)
+    assert st['n_blob16'] == 0 and len(st['blobs']) == 0
+    A32 = sp.csr_matrix(A, dtype=np.float32)
+    boo = S.csr_to_boo(A32, cluster='identity', target_nr=32, target_nc=32)
+    st = _core.boo_stage(_host(boo), 4096, 256, 64, 1, 1.5)
+    assert st['n_blob16'] == 0
+
+
+def test_stage_rejects_out_of_range_columns():
+    """Column ids and remainder columns out of [0, cols), and a decreasing
+    remainder row pointer, are errors of the staging call (SPMM_EINVAL ->
+    ValueError), never an out-of-range host access."""
+    n = 2000
+    A = sp.diags([np.ones(n - 1), 2 * np.ones(n), np.ones(n - 1)], [-1, 0, 1], format='csr', dtype=np.float32)
+    A = M.permuted(A, seed=1)
+    boo = S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32)
+    good = _host(boo)
+    _core.boo_stage(good, 4096, 256, 64, 4, 1.5)                 # the unmodified input stages
+    assert good['rem_col_ind'].size > 0
+    for key, idx, val in (('rem_col_ind', 0, -2 ** 30), ('rem_col_ind', -1, n), ('col_ids', 3, n + 7),
+                          ('col_ids', 0, -1)):
+        h = dict(good)
+        h[key] = good[key].copy()
+        h[key][idx] = val
+        with pytest.raises(ValueError, match='out of range'):
+            _core.boo_stage(h, 4096, 256, 64, 4, 1.5)
+    h = dict(good)
+    h['rem_indptr'] = good['rem_indptr'].copy()
+    r = int(np.nonzero(np.diff(h['rem_indptr']) > 0)[0][0])
+    h['rem_indptr'][r + 1] = h['rem_indptr'][r] - 1
+    with pytest.raises(ValueError, match='nondecreasing|start'):
+        _core.boo_stage(h, 4096, 256, 64, 4, 1.5)

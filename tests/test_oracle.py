@@ -12,6 +12,7 @@ import scipy.sparse as sp
 
 from conftest import csr_of, fixture_names, load_fixture
 from oracle import oracle as O
+from spmm_amd import matrices as M
 
 
 # ---------------------------------------------------------------- labels
@@ -225,3 +226,38 @@ def test_within_bound_detects_a_planted_error():
     assert ok and ratio < 1e-6
     y[3, 2] += 1e-3 * (abs(m) @ abs(x))[3, 2] + 1e-3
     assert not O.within_bound(y, m, x)[1]
+
+
+def test_reference_product_leaves_unsorted_input_untouched():
+    """A CSR whose rows are not sorted (P A P^T with fancy indexing) must
+    come out of spmm_reference unchanged, and the product must equal the
+    dense product every time (scipy canonicalises matrices in place, and a
+    dtype-converting csr_matrix(...) shares the caller's index arrays)."""
+    A0 = M.stencil_27pt(10)
+    n = A0.shape[0]
+    perm = np.random.default_rng(4).permutation(n)
+    A = sp.csr_matrix(A0[perm][:, perm])
+    assert not A.has_sorted_indices
+    before = (A.indptr.copy(), A.indices.copy(), A.data.copy())
+    x = M.dense_x(n, 32, seed=3)
+    dense = A.toarray().astype(np.float64) @ x.astype(np.float64)
+    for _ in range(3):
+        ref, bound = O.spmm_reference(A, x)
+        assert np.abs(ref - dense).max() < 1e-12
+        assert np.all(bound >= np.abs(ref))
+        for a, b in zip(before, (A.indptr, A.indices, A.data)):
+            assert np.array_equal(a, b)
+
+
+def test_builders_leave_unsorted_input_untouched():
+    import spmm_amd as S
+    A0 = M.stencil_27pt(8)
+    n = A0.shape[0]
+    perm = np.random.default_rng(1).permutation(n)
+    A = sp.csr_matrix(A0[perm][:, perm])
+    assert not A.has_sorted_indices
+    before = (A.indptr.copy(), A.indices.copy(), A.data.copy())
+    S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32)
+    S.csr_to_pbr(A, 8, 8, 4)
+    for a, b in zip(before, (A.indptr, A.indices, A.data)):
+        assert np.array_equal(a, b)
