@@ -147,14 +147,15 @@ int spmm_boo_stage_copy(const spmm_boo_stage* st, int32_t* tiles, uint16_t* tile
                         int32_t* gtask_ptr);
 /* The record stream of a float matrix staged with group 4 (n_blob16 > 0): the
  * same tiles as above, one contiguous 16-byte aligned record per wave and
- * step (that step's entries, row starts, the ids of the X rows the wave
- * stages and, at an item's end, the slice's row ids), so that the fastest
- * kernel moves a whole step into LDS with one DMA instruction.
+ * step (that step's entries, row starts and the slice's first row), so that
+ * a kernel moves a whole step into LDS with one DMA instruction, and beside
+ * it the ids of the X rows each wave stages at each step.
  *   blobs [n_blob16*16] bytes, blob_first [n_waves*8] uint32 (per wave: the
- *   offsets of its first 4 records, their sizes, its step count).
+ *   offsets of its first 4 records, their sizes, its step count, its first
+ *   tile), blob_xid [n_tiles*8] uint32.
  * Optional: a descriptor without it runs the same tiles through the other
- * kernels (same results within the stated tolerance, slower). */
-int spmm_boo_stage_copy_blobs(const spmm_boo_stage* st, void* blobs, uint32_t* blob_first);
+ * kernels (same results within the stated tolerance). */
+int spmm_boo_stage_copy_blobs(const spmm_boo_stage* st, void* blobs, uint32_t* blob_first, uint32_t* blob_xid);
 void spmm_boo_stage_destroy(spmm_boo_stage* st);
 
 /* Device descriptor: the staged arrays plus row_ids and the remainder CSR
@@ -196,6 +197,7 @@ typedef struct spmm_boo_desc {
     int64_t n_blob16;            /* record stream (spmm_boo_stage_copy_blobs); 0 and NULLs: none */
     const void* blobs;           /* [n_blob16*16] bytes */
     const uint32_t* blob_first;  /* [n_waves*8] */
+    const uint32_t* blob_xid;    /* [n_tiles*8] */
 } spmm_boo_desc;
 
 /* Workspace bytes spmm_boo_matmul needs for this staging and shape: the

@@ -217,7 +217,7 @@ def _kernel_staging(rows, cols, d, rowmajor, row_ids_dev, device, rem_dev=None):
              'wave_tiles', 'crow_ptr', 'crow_id', 'ccol', 'cval', 'gtask', 'gtask_ptr']
     records = RECORD_STREAM and int(stage['n_blob16']) > 0
     if records:
-        names += ['blobs', 'blob_first']
+        names += ['blobs', 'blob_first', 'blob_xid']
     g = types.SimpleNamespace(**{k: _pinned(stage[k], device) for k in names})
     if rem_dev is None:
         rem_dev = (_pinned(k_rem_indptr, device), _pinned(k_rem_col, device), _pinned(k_rem_val, device))
@@ -238,6 +238,7 @@ def _kernel_staging(rows, cols, d, rowmajor, row_ids_dev, device, rem_dev=None):
         'rem_indptr': p(rem_dev[0]), 'rem_col_ind': p(rem_dev[1]), 'rem_vals': p(rem_dev[2]),
         'n_blob16': int(stage['n_blob16']) if records else 0,
         'blobs': p(g.blobs) if records else 0, 'blob_first': p(g.blob_first) if records else 0,
+        'blob_xid': p(g.blob_xid) if records else 0,
     }
     return g, rem_dev, desc
 

@@ -47,12 +47,12 @@ namespace spmm_stage {
 
 constexpr int TILE_ROWS = 32;
 constexpr int TILE_COLS = 32;
-constexpr int TILE_ENT = 128;
+constexpr int TILE_ENT = 96;
 constexpr int TILE_RS = TILE_ROWS + 1;
 constexpr int TILE_WORDS = 8;
 constexpr uint32_t FLAG_LAST = 1u;    // last tile of its item
 constexpr uint32_t FLAG_SERIAL = 2u;  // computed one busy row at a time
-constexpr int SERIAL_MAX_BUSY = 8;    // busy rows a serial tile may have
+constexpr int SERIAL_MAX_BUSY = 4;    // busy rows a serial tile may have
 
 // Cost model for dealing groups to workgroups, in units of one entry's work:
 // a step (X tile staged, workgroup synchronised) and finishing an item.
@@ -85,25 +85,27 @@ constexpr int GATHER_SKEWED_LONG = 32;
 constexpr int GATHER_REUSE_WINDOW = 8192;
 constexpr double GATHER_REORDER_GAIN = 2.0;
 
-// Blob stream (float, groups of 4): each wave's tiles again, one contiguous,
-// 16-byte aligned record per step, so that a wave moves a whole step's data
-// into LDS with one DMA instruction.  A record:
+// Record stream (float, groups of 4): each wave's tiles again, one
+// contiguous, 16-byte aligned record per step, so that a wave moves a whole
+// step's entries into LDS with one DMA instruction, and beside it the ids of
+// the X rows the wave stages at each step (8 per tile), so that the X tile
+// can be staged without waiting for the step's record.  A record:
 //   word 0   nnz | nr << 8 | nc << 14 | flags << 20 | nvec(record 4 steps later) << 24
 //   word 1   slot (-1: the item stores Y)
 //   word 2   offset, in 16-byte units, of this wave's record 4 steps later
 //            (clamped to its last record)
-//   word 3   CONTIG: global id of the step's first X column (column c is
-//            id + min(c, nc - 1)); otherwise 0
-//   int32 cid[8]      (absent when CONTIG) X rows this wave stages in the step's
-//                     tile: entry j names column 2m + (j >> 2) + 8 (j & 3),
-//                     m = the wave's index in its workgroup, clamped to nc - 1
+//   word 3   ROWCONTIG: the slice's first Y row (row r is that + r);
+//            otherwise its offset into row_ids
 //   uint8 rs[32]      (absent when nnz = 0) first entry of each row; row r
 //                     ends at rs[r + 1], row 31 at nnz
-//   int32 row_id[32]  (ROWIDS only) Y rows of the slice, for the store
 //   uint8 col[nnz]    local columns, then zero padding to 4 bytes
 //   float val[nnz]    then zero padding to 16 bytes
-constexpr uint32_t BLOB_LAST = 1u, BLOB_SERIAL = 2u, BLOB_ROWIDS = 4u, BLOB_CONTIG = 8u;
-constexpr int BLOB_MAX_BYTES = 16 + 32 + 32 + 128 + TILE_ENT + 4 * TILE_ENT;  // 848
+// The X ids of tile t (the wave's tile index, as in tiles): xid[8 t + j] is
+// the X row of column 2m + (j >> 2) + 8 (j & 3) of the step's X tile, m the
+// wave's index in its workgroup, clamped to the tile's last column (X row 0
+// for a tile without columns).
+constexpr uint32_t BLOB_LAST = 1u, BLOB_SERIAL = 2u, BLOB_ROWCONTIG = 4u;
+constexpr int BLOB_MAX_BYTES = 16 + 32 + TILE_ENT + 4 * TILE_ENT;  // 528
 constexpr int BLOB_LOOKAHEAD = 4;
 
 
@@ -133,12 +135,13 @@ struct Staged {
     int32_t n_waves = 0;
     int32_t group = 1;               // waves per workgroup sharing X tiles
     int32_t n_stream_rows = 0;       // rows the tile stream stores (the rest: crow_id)
-    // blob stream (float, group 4; empty otherwise): records in 16-byte units
-    // (4 words each), and per wave 8 words: offsets of its first 4 records
+    // record stream (float, group 4; empty otherwise): records in 16-byte
+    // units (4 words each); per wave 8 words: offsets of its first 4 records
     // (clamped to its last), their 16-byte counts packed one per byte, its
-    // step count, 0, 0
+    // step count, its first tile, 0; and the X ids, 8 per tile
     std::vector<uint32_t> blobs;
     std::vector<uint32_t> blob_first;
+    std::vector<uint32_t> blob_xid;
     size_t n_tiles() const { return tiles.size() / TILE_WORDS; }
 };
 
@@ -618,7 +621,9 @@ private:
     }
 
     // Cut a member's entries [e0, e1) of tent_ (row-major) between rows into
-    // pieces of at most TILE_ENT entries.
+    // pieces of at most TILE_ENT entries; a row longer than that on its own
+    // (duplicate entries) is cut inside, its parts in consecutive pieces of the
+    // same item, so it keeps accumulating in the same registers.
     static void cut(const std::vector<Ent>& v, size_t e0, size_t e1, std::vector<Piece>& out) {
         size_t i = e0;
         do {
@@ -626,7 +631,10 @@ private:
             while (i < e1) {
                 size_t j = i;
                 while (j < e1 && v[j].lr == v[i].lr) ++j;
-                if (j - start > (size_t)TILE_ENT && i > start) break;
+                if (j - start > (size_t)TILE_ENT) {
+                    if (i == start) i = start + TILE_ENT;
+                    break;
+                }
                 i = j;
             }
             out.push_back(Piece{start, i});
@@ -895,8 +903,10 @@ private:
     void emit_blobs(Staged& S) {
         S.blobs.clear();
         S.blob_first.clear();
+        S.blob_xid.clear();
         if (!std::is_same<T, float>::value || G_ != 4 || S.n_waves <= 0) return;
         S.blob_first.assign((size_t)S.n_waves * 8, 0u);
+        S.blob_xid.assign(S.n_tiles() * 8, 0u);
         std::vector<uint32_t> offs, nvec;
         std::vector<uint8_t> rec;
         for (int w = 0; w < S.n_waves; ++w) {
@@ -911,50 +921,38 @@ private:
                 const int nnz = (int)(w1 & 0xffu), nc = (int)((w1 >> 8) & 0xffu), nr = (int)((w1 >> 16) & 0xffu);
                 const uint32_t tflags = w1 >> 24;
                 const int cid_off = tw[2], row_off = tw[3], slot = tw[4];
+                // the X rows this wave stages at this step
+                for (int j = 0; j < 8; ++j) {
+                    const int c = std::min(2 * m + (j >> 2) + 8 * (j & 3), nc - 1);
+                    S.blob_xid[(size_t)t * 8 + j] = nc > 0 ? (uint32_t)S.tcols[(size_t)cid_off + c] : 0u;
+                }
                 uint32_t flags = 0;
                 if (tflags & FLAG_LAST) flags |= BLOB_LAST;
                 if (tflags & FLAG_SERIAL) flags |= BLOB_SERIAL;
-                const bool rowids = (tflags & FLAG_LAST) && slot < 0 && nr > 0;
-                if (rowids) flags |= BLOB_ROWIDS;
-                // X columns: contiguous ids need only the first
-                bool contig = true;
-                int ncx = nc;
-                int32_t base = 0;
-                if (nc == 0) {
-                    ncx = 1;          // nothing to stage: load X row 0, never read
-                } else {
-                    base = S.tcols[(size_t)cid_off];
-                    for (int c = 1; c < nc && contig; ++c) contig = S.tcols[(size_t)cid_off + c] == base + c;
-                }
-                if (contig) flags |= BLOB_CONTIG;
+                bool rcontig = nr > 0;
+                for (int r = 1; r < nr && rcontig; ++r) rcontig = in_.row_ids[row_off + r] == in_.row_ids[row_off] + r;
+                if (rcontig) flags |= BLOB_ROWCONTIG;
                 rec.clear();
                 auto put32 = [&](uint32_t v) {
                     for (int k = 0; k < 4; ++k) rec.push_back((uint8_t)(v >> (8 * k)));
                 };
-                put32((uint32_t)nnz | (uint32_t)nr << 8 | (uint32_t)ncx << 14 | flags << 20);
+                put32((uint32_t)nnz | (uint32_t)nr << 8 | (uint32_t)std::min(nc, 63) << 14 | flags << 20);
                 put32((uint32_t)slot);
                 put32(0u);            // patched below
-                put32(contig ? (uint32_t)base : 0u);
-                if (!contig)
-                    for (int j = 0; j < 8; ++j) {
-                        const int c = std::min(2 * m + (j >> 2) + 8 * (j & 3), nc - 1);
-                        put32((uint32_t)S.tcols[(size_t)cid_off + c]);
-                    }
+                put32(rcontig ? (uint32_t)in_.row_ids[row_off] : (uint32_t)row_off);
                 if (nnz > 0)
                     for (int r = 0; r < TILE_ROWS; ++r) {
                         const uint16_t v = S.tile_rs[(size_t)t * TILE_RS + r];
                         if (v > 255) throw std::invalid_argument("tile row start exceeds a byte");
                         rec.push_back((uint8_t)v);
                     }
-                if (rowids)
-                    for (int r = 0; r < TILE_ROWS; ++r) put32(r < nr ? (uint32_t)in_.row_ids[row_off + r] : 0u);
                 for (int e = 0; e < nnz; ++e) rec.push_back(S.ent_col[(size_t)ent_off + e]);
                 while (rec.size() & 3) rec.push_back(0);
                 const size_t vbytes = (size_t)nnz * sizeof(T);
                 const char* vp = S.ent_val.data() + (size_t)ent_off * sizeof(T);
                 rec.insert(rec.end(), vp, vp + vbytes);
                 while (rec.size() & 15) rec.push_back(0);
-                if ((int)rec.size() > BLOB_MAX_BYTES) throw std::invalid_argument("blob record too large");
+                if ((int)rec.size() > BLOB_MAX_BYTES) throw std::invalid_argument("record too large");
                 offs.push_back((uint32_t)(S.blobs.size() / 4));
                 nvec.push_back((uint32_t)(rec.size() / 16));
                 const size_t at = S.blobs.size();
@@ -979,10 +977,13 @@ private:
                 f[4] = packed;
             }
             f[5] = (uint32_t)n;
+            f[6] = (uint32_t)t0;
         }
-        if (S.blobs.size() / 4 + 64 >= (size_t)1 << 28) {   // 4 GiB: DMA offsets are 32-bit bytes
+        // DMA offsets are 32-bit byte offsets: records and X ids under 4 GiB
+        if (S.blobs.size() / 4 + 64 >= (size_t)1 << 28 || S.n_tiles() + 64 >= (size_t)1 << 27) {
             S.blobs.clear();
             S.blob_first.clear();
+            S.blob_xid.clear();
         }
     }
 

@@ -303,6 +303,7 @@ spmm_boo_desc boo_desc(const py::dict& d) {
         A.n_blob16 = d["n_blob16"].cast<int64_t>();
         A.blobs = reinterpret_cast<const void*>(P(d, "blobs"));
         A.blob_first = reinterpret_cast<const uint32_t*>(P(d, "blob_first"));
+        A.blob_xid = reinterpret_cast<const uint32_t*>(P(d, "blob_xid"));
     }
     return A;
 }
@@ -355,14 +356,16 @@ py::dict boo_stage(const py::dict& h, int32_t max_item_nnz, int32_t long_thresho
                                        ecol.data(), tcols.data(), splits.data(), longr.data(), wt.data(),
                                        crp.data(), cri.data(), ccol.data(),
                                        inf.n_cnz ? cv.mutable_data() : nullptr, gt.data(), gtp.data());
-    std::vector<uint32_t> blobs((size_t)inf.n_blob16 * 4), bfirst(inf.n_blob16 > 0 ? (size_t)inf.n_waves * 8 : 0);
-    const int rc2 = rc ? rc : spmm_boo_stage_copy_blobs(st, blobs.data(), bfirst.data());
+    std::vector<uint32_t> blobs((size_t)inf.n_blob16 * 4), bfirst(inf.n_blob16 > 0 ? (size_t)inf.n_waves * 8 : 0),
+        bxid(inf.n_blob16 > 0 ? (size_t)inf.n_tiles * 8 : 0);
+    const int rc2 = rc ? rc : spmm_boo_stage_copy_blobs(st, blobs.data(), bfirst.data(), bxid.data());
     spmm_boo_stage_destroy(st);
     raise_status(rc);
     raise_status(rc2);
     py::dict d;
     d["blobs"] = give(std::move(blobs));
     d["blob_first"] = give(std::move(bfirst));
+    d["blob_xid"] = give(std::move(bxid));
     d["n_blob16"] = inf.n_blob16;
     d["tiles"] = give(std::move(tiles));
     d["tile_rs"] = give(std::move(rs));

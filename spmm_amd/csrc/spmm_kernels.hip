@@ -142,7 +142,7 @@ inline int round_up8(long long n) { return (int)((n + 7) / 8 * 8); }
 
 constexpr int ST_ROWS = 32;   // rows of a tile / an item slice (2 lanes per row)
 constexpr int ST_COLS = 32;   // columns (X rows) of a tile
-constexpr int ST_ENT = 128;   // entries of a tile
+constexpr int ST_ENT = 96;    // entries of a tile
 constexpr int ST_RS = 33;     // row-start table length
 constexpr int ST_WORDS = 8;   // metadata words per tile
 constexpr int ST_FLAG_LAST = 1;     // last tile of its item: store the rows
@@ -163,6 +163,7 @@ struct StreamArgs {
     T* P;
     const uint32_t* blobs;       // record stream (float, group 4), or null
     const uint32_t* blob_first;
+    const uint32_t* blob_xid;
 };
 
 // &Xb[row*K + f].  A32: the X slab of one batch is under 4 GiB, so the byte
@@ -364,7 +365,7 @@ __device__ __forceinline__ void st_row(T (&acc)[F / VEC][VEC], int j, int e, con
     }
 }
 
-constexpr int ST_SYN = 8;   // busy rows a serial tile may have
+constexpr int ST_SYN = 4;   // busy rows a serial tile may have
 
 // A tile whose entries sit in a few busy rows: the whole wave takes one busy
 // row at a time with lanes along the tile's features, and leaves the row's
@@ -804,36 +805,48 @@ __global__ void __launch_bounds__(256, 4) boo_stream_dma_kernel(StreamArgs<float
 // ---------------------------------------------------------------------------
 // BOO tile stream, float, 64-feature tiles, every load a DMA into LDS.
 //
-// The same groups and lock step as boo_stream_dma_kernel, but a wave's whole
-// share of a step -- entries, row starts, the ids of the X rows it stages and,
-// at an item's end, the slice's row ids -- is one contiguous record of the
-// blob stream (boo_stage.hpp), moved into LDS by a single
-// global_load_lds_dwordx4 BLOB_LOOKAHEAD = 4 steps ahead; the step's X tile
-// is moved DX steps ahead into a ring of DX + 1 tiles.  No load lands in a
-// register, so every wait is explicit and counted: at the top of step t a
-// wave needs what it issued two steps earlier (DX = 2: its share of X tile
-// t, and record t + 2 whose column ids name the X rows of tile t + 2) and
-// lets the later step's X share, stores and record stay in flight.  Y rows
+// The same groups and lock step as boo_stream_dma_kernel, but no load lands
+// in a register, so every wait is explicit and counted, and every wait is for
+// loads issued two or more steps earlier.  Three streams per wave, all moved
+// into LDS by global_load_lds:
+//   * records (boo_stage.hpp): a step's entries and row starts, one DMA
+//     instruction each, BLOB_LOOKAHEAD = 4 steps ahead;
+//   * X ids: the 8 X rows the wave stages for a step, 32 bytes, XID_AHEAD = 5
+//     steps ahead (they only address the X tile, so they never wait for a
+//     record);
+//   * X tiles: the wave's 2 of the tile's 8 DMA instructions, DX = 2 steps
+//     ahead, into a ring of 3 tiles shared by the workgroup.
+// Per step a wave issues, in this order: X(n + 2) (top, right after the
+// barrier), then at the bottom its Y stores (8, at an item's end), record
+// n + 4 and X ids n + 5.  At the top of step n it needs X(n) from every wave,
+// record n and X ids n + 2; in issue order everything after X(n) may still be
+// in flight: 6 operations plus the stores of steps n - 2 and n - 1.  Y rows
 // are written by inline-asm stores so that their count is known exactly.
-// Per step a wave issues: its 2 X DMA instructions (top), at an item's end
-// 8 stores, then the DMA of record t + 4 into the buffer record t used
-// (bottom).
 // ---------------------------------------------------------------------------
 
-constexpr int BLOB_BUF = 864;   // LDS bytes per record buffer (>= the largest record + read-ahead)
-constexpr uint32_t BL_LAST = 1u, BL_SERIAL = 2u, BL_ROWIDS = 4u, BL_CONTIG = 8u;
+constexpr int BLOB_BUF = 544;    // LDS bytes per record buffer (the largest record, 528, + read-ahead)
+constexpr uint32_t BL_LAST = 1u, BL_SERIAL = 2u, BL_ROWCONTIG = 4u;
+constexpr int SYN_STRIDE = 272;  // bytes per serial-row sum (64 floats + 16)
+constexpr int XID_RING = 8;      // X-id slots per wave (32 bytes each)
+constexpr int XID_AHEAD = 5;
 
+// DX + 1 X tiles + 16 serial rows + 16 records + 32 X-id slots: 39,424
+// bytes at DX = 2 (four workgroups, 16 waves, per CU), 30,976 at DX = 1
+// (five workgroups, 20 waves).
 template <int DX>
 struct StBlobLds {
-    float xt[DX + 1][8 * DMA_BLK / 4];    // X tile ring
-    float syn[8 * DMA_BLK / 4];            // serial rows: wave w's are columns 8w .. 8w+7
-    uint8_t rec[4][4][BLOB_BUF];           // [wave][step mod 4] record buffers
+    float xt[DX + 1][8 * DMA_BLK / 4];         // X tile ring
+    float syn[4 * ST_SYN * SYN_STRIDE / 4];    // serial rows: wave w's are rows ST_SYN w ..
+    uint8_t rec[4][4][BLOB_BUF];               // [wave][step mod 4] records
+    uint32_t xid[4][XID_RING][8];              // [wave][step mod 8] X ids
 };
 
 struct BlobArgs {
     int rows, cols, K, batch, n_waves;
     const uint32_t* blobs;   // records, 16-byte units
     const uint32_t* first;   // [n_waves][8]
+    const uint32_t* xid;     // [n_tiles][8]
+    const int* row_ids;
     const float* X;
     float* Y;
     float* P;
@@ -862,7 +875,7 @@ __device__ __forceinline__ void store8(float* p, const f4_t (&d)[8]) {
 }
 
 template <int DX>
-__global__ void __launch_bounds__(256, DX >= 2 ? 3 : 4) boo_blob_kernel(BlobArgs a, int kt0) {
+__global__ void __launch_bounds__(256, DX == 1 ? 5 : 4) boo_blob_kernel(BlobArgs a, int kt0) {
     static_assert(DX == 1 || DX == 2, "X tiles are staged 1 or 2 steps ahead");
     __shared__ __attribute__((aligned(16))) StBlobLds<DX> L;
     const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -871,12 +884,13 @@ __global__ void __launch_bounds__(256, DX >= 2 ? 3 : 4) boo_blob_kernel(BlobArgs
     // the wave's 8 words, held in SGPRs before any DMA: a vector load here
     // would enter the counted waits below
     const uint32_t* F = a.first + 8 * (size_t)w;
-    uint32_t fw[6];
+    uint32_t fw[7];
 #pragma unroll
-    for (int k = 0; k < 6; ++k) fw[k] = (uint32_t)__builtin_amdgcn_readfirstlane((int)F[k]);
-    asm volatile("" ::"s"(fw[0]), "s"(fw[1]), "s"(fw[2]), "s"(fw[3]), "s"(fw[4]), "s"(fw[5]));
+    for (int k = 0; k < 7; ++k) fw[k] = (uint32_t)__builtin_amdgcn_readfirstlane((int)F[k]);
+    asm volatile("" ::"s"(fw[0]), "s"(fw[1]), "s"(fw[2]), "s"(fw[3]), "s"(fw[4]), "s"(fw[5]), "s"(fw[6]));
     const int nsteps = (int)fw[5];
     if (nsteps <= 0) return;     // uniform per workgroup: its streams have equal lengths
+    const uint32_t t0 = fw[6];
     const int lane = threadIdx.x & 63;
     const int h = lane & 1;
     const int lr = lane >> 1;
@@ -887,57 +901,65 @@ __global__ void __launch_bounds__(256, DX >= 2 ? 3 : 4) boo_blob_kernel(BlobArgs
     const uint32_t rowb = (uint32_t)K * 4u;
     const uint32_t lane_x = (uint32_t)fbase * 4u + (uint32_t)(lane & 15) * 16u;
     const int kq = lane >> 4;  // column I + 8 kq of DMA instruction I
-    const uint32_t x_lds = lds_u32(&L.xt[0][0]);
+    const uint32_t x_lds = lds_u32(&L.xt[0][0]) + (uint32_t)(2 * wv) * DMA_BLK;
+    const uint32_t rec_lds = lds_u32(&L.rec[wv][0][0]);
+    const uint32_t xid_lds = lds_u32(&L.xid[wv][0][0]);
+    const int last = nsteps - 1;
 
-    auto rec_ptr = [&](int n) { return &L.rec[wv][n & 3][0]; };
     auto issue_rec = [&](uint32_t off16, uint32_t nvec, int n) {
         if ((uint32_t)lane < nvec)
             dma16(reinterpret_cast<const float*>(a.blobs), off16 * 16u + (uint32_t)lane * 16u,
-                  (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_u32(rec_ptr(n))));
+                  (uint32_t)__builtin_amdgcn_readfirstlane((int)(rec_lds + (uint32_t)(n & 3) * BLOB_BUF)));
     };
-    // this wave's two DMA instructions (2 wv, 2 wv + 1) of X tile n, whose
-    // column ids are in record n
+    // X ids of step n (clamped to the last): 32 bytes, lanes 0 and 1
+    auto issue_xid = [&](int n) {
+        const uint32_t t = t0 + (uint32_t)min(n, last);
+        if (lane < 2)
+            dma16(reinterpret_cast<const float*>(a.xid), t * 32u + (uint32_t)lane * 16u,
+                  (uint32_t)__builtin_amdgcn_readfirstlane((int)(xid_lds + (uint32_t)(n & (XID_RING - 1)) * 32u)));
+    };
+    // this wave's two DMA instructions (2 wv, 2 wv + 1) of X tile n
     auto issue_x = [&](int n) {
-        const uint8_t* rp = rec_ptr(n);
-        const uint32_t w0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)*reinterpret_cast<const uint32_t*>(rp));
-        const uint32_t nc = (w0 >> 14) & 63u;
-        uint32_t id0, id1;
-        if ((w0 >> 20) & BL_CONTIG) {
-            const uint32_t base =
-                (uint32_t)__builtin_amdgcn_readfirstlane((int)*reinterpret_cast<const uint32_t*>(rp + 12));
-            const uint32_t c0 = (uint32_t)(2 * wv + 8 * kq);
-            id0 = base + min(c0, nc - 1u);
-            id1 = base + min(c0 + 1u, nc - 1u);
-        } else {
-            const uint32_t* cid = reinterpret_cast<const uint32_t*>(rp + 16);
-            id0 = cid[kq];
-            id1 = cid[4 + kq];
-        }
-        const uint32_t l0 = x_lds + (uint32_t)(n % (DX + 1)) * (8u * DMA_BLK) + (uint32_t)(2 * wv) * DMA_BLK;
+        const uint32_t* ids = &L.xid[wv][n & (XID_RING - 1)][0];
+        const uint32_t id0 = ids[kq], id1 = ids[4 + kq];
+        const uint32_t l0 = x_lds + (uint32_t)(n % (DX + 1)) * (8u * DMA_BLK);
         dma16(Xb, __umul24(id0, rowb) + lane_x, l0);
         dma16(Xb, __umul24(id1, rowb) + lane_x, l0 + (uint32_t)DMA_BLK);
     };
 
-    // prologue: the last operations before step 0 are laid out as the steady
-    // state leaves them, so step 0 waits like any other step
+    // prologue: the operations before step 0 are laid out as the steady
+    // state leaves them (after X(0): record 2, ids 3, X(1), record 3, ids 4),
+    // so step 0 waits like any other step
     {
         const uint32_t nv = fw[4];
         if constexpr (DX == 2) {
+            // after X(0): record 2, ids 3, X(1), record 3, ids 4
+            issue_xid(0);
+            issue_xid(1);
+            issue_xid(2);
             issue_rec(fw[0], nv & 0xffu, 0);
             issue_rec(fw[1], (nv >> 8) & 0xffu, 1);
-            wait_vm<1>();                       // record 0
+            wait_vm<4>();                       // ids 0
             issue_x(0);
             issue_rec(fw[2], (nv >> 16) & 0xffu, 2);
-            wait_vm<3>();                       // record 1
+            issue_xid(3);
+            wait_vm<7>();                       // ids 1
             issue_x(1);
             issue_rec(fw[3], nv >> 24, 3);
+            issue_xid(4);
         } else {
+            // after X(0): record 3, ids 4
+            issue_xid(0);
+            issue_xid(1);
+            issue_xid(2);
             issue_rec(fw[0], nv & 0xffu, 0);
             issue_rec(fw[1], (nv >> 8) & 0xffu, 1);
             issue_rec(fw[2], (nv >> 16) & 0xffu, 2);
-            wait_vm<2>();                       // record 0
+            issue_xid(3);
+            wait_vm<6>();                       // ids 0
             issue_x(0);
             issue_rec(fw[3], nv >> 24, 3);
+            issue_xid(4);
         }
     }
 
@@ -946,42 +968,43 @@ __global__ void __launch_bounds__(256, DX >= 2 ? 3 : 4) boo_blob_kernel(BlobArgs
     for (int q = 0; q < 8; ++q) acc[q] = f4_t{0.f, 0.f, 0.f, 0.f};
 
     typedef __attribute__((address_space(3))) const char lds_char;
-    bool stored_prev = false;
+    int st1 = 0, st2 = 0;   // stores issued by steps n - 1 and n - 2 (0 or 8 each)
     for (int n = 0; n < nsteps; ++n) {
-        // (1) X tile n (every wave's share) and record n + DX (own) are in
+        // (1) X tile n (every wave's share), record n and ids n + 2 are in
         // LDS; the barrier publishes the tile
         if constexpr (DX == 2) {
-            if (stored_prev) asm volatile("s_waitcnt vmcnt(11) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-            else asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            // after X(n): ops of steps n - 2 (bottom) and n - 1
+            const int pend = st1 + st2;
+            if (pend == 0) asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            else if (pend == 8) asm volatile("s_waitcnt vmcnt(14) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            else asm volatile("s_waitcnt vmcnt(22) lgkmcnt(0)\n\ts_barrier" ::: "memory");
         } else {
-            if (stored_prev) asm volatile("s_waitcnt vmcnt(9) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-            else asm volatile("s_waitcnt vmcnt(1) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            // after X(n): the bottom of step n - 1
+            if (st1 == 0) asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            else asm volatile("s_waitcnt vmcnt(10) lgkmcnt(0)\n\ts_barrier" ::: "memory");
         }
         __builtin_amdgcn_sched_barrier(0);
         // (2) X tile n + DX into the buffer tile n - 1 used
         issue_x(n + DX);
         __builtin_amdgcn_sched_barrier(0);
         // (3) record n
-        const uint8_t* rp = rec_ptr(n);
-        const uint32_t w0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)*reinterpret_cast<const uint32_t*>(rp));
-        const int slot = __builtin_amdgcn_readfirstlane((int)*reinterpret_cast<const uint32_t*>(rp + 4));
-        const uint32_t next_off =
-            (uint32_t)__builtin_amdgcn_readfirstlane((int)*reinterpret_cast<const uint32_t*>(rp + 8));
+        const uint8_t* rp = &L.rec[wv][n & 3][0];
+        const uint4 hd = *reinterpret_cast<const uint4*>(rp);
+        const uint32_t w0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)hd.x);
+        const int slot = __builtin_amdgcn_readfirstlane((int)hd.y);
+        const uint32_t next_off = (uint32_t)__builtin_amdgcn_readfirstlane((int)hd.z);
+        const int rbase = __builtin_amdgcn_readfirstlane((int)hd.w);
         const int nnz = (int)(w0 & 0xffu);
         const int nr = (int)((w0 >> 8) & 63u);
         const uint32_t fl = (w0 >> 20) & 15u;
         const uint32_t next_nvec = w0 >> 24;
-        int p = 16 + ((fl & BL_CONTIG) ? 0 : 32);
-        const int p_rs = p;
-        p += nnz > 0 ? 32 : 0;
-        const int p_rid = p;
-        p += (fl & BL_ROWIDS) ? 128 : 0;
-        const uint8_t* cols = rp + p;
-        const float* vals = reinterpret_cast<const float*>(rp + p + ((nnz + 3) & ~3));
+        const int p_cols = nnz > 0 ? 48 : 16;
+        const uint8_t* cols = rp + p_cols;
+        const float* vals = reinterpret_cast<const float*>(rp + p_cols + ((nnz + 3) & ~3));
         int rs0 = 0, rs1 = 0;
         if (nnz > 0) {
-            rs0 = rp[p_rs + lr];
-            rs1 = lr == ST_ROWS - 1 ? nnz : (int)rp[p_rs + lr + 1];
+            rs0 = rp[16 + lr];
+            rs1 = lr == ST_ROWS - 1 ? nnz : (int)rp[16 + lr + 1];
         }
         const float* tile = &L.xt[n % (DX + 1)][0];
         // (4) the walk
@@ -1003,13 +1026,13 @@ __global__ void __launch_bounds__(256, DX >= 2 ? 3 : 4) boo_blob_kernel(BlobArgs
                     s1 += vals[j + 1] * *reinterpret_cast<const float*>(xc + dma_col_off(c1));
                 }
                 if (j < e) s0 += vals[j] * *reinterpret_cast<const float*>(xc + dma_col_off(cols[j]));
-                *reinterpret_cast<float*>(reinterpret_cast<char*>(L.syn) + dma_col_off(8 * wv + k) + lane * 4) =
-                    s0 + s1;
+                *reinterpret_cast<float*>(reinterpret_cast<char*>(L.syn) + (ST_SYN * wv + k) * SYN_STRIDE +
+                                          lane * 4) = s0 + s1;
                 if ((lane & ~1) == l2) mine = k;
             }
             wave_lds_fence();
             if (mine >= 0) {
-                lds_char* sr = (lds_char*)(L.syn) + dma_col_off(8 * wv + mine) + h * 16;
+                lds_char* sr = (lds_char*)(L.syn) + (ST_SYN * wv + mine) * SYN_STRIDE + h * 16;
                 const f4_t* xr = (const f4_t*)sr;
                 f4_t x[8];
 #pragma unroll
@@ -1040,12 +1063,16 @@ __global__ void __launch_bounds__(256, DX >= 2 ? 3 : 4) boo_blob_kernel(BlobArgs
         }
         wave_lds_fence();
         // (5) end of the item: store its rows
-        stored_prev = false;
+        st2 = st1;
+        st1 = 0;
         if ((fl & BL_LAST) && nr > 0) {
             if (lr < nr) {
                 float* out;
                 if (slot < 0) {
-                    const int row = *reinterpret_cast<const int*>(rp + p_rid + 4 * lr);
+                    // row ids not consecutive: a plain load, waited for at once
+                    // (the compiler's wait also drains this wave's DMAs, so
+                    // the counts below only get more conservative)
+                    const int row = (fl & BL_ROWCONTIG) ? rbase + lr : a.row_ids[rbase + lr];
                     out = a.Y + ((size_t)b * a.rows + row) * K + fbase + h * 4;
                 } else {
                     out = a.P + (((size_t)slot * a.batch + b) * ST_ROWS + lr) * K + fbase + h * 4;
@@ -1054,12 +1081,14 @@ __global__ void __launch_bounds__(256, DX >= 2 ? 3 : 4) boo_blob_kernel(BlobArgs
             }
 #pragma unroll
             for (int q = 0; q < 8; ++q) acc[q] = f4_t{0.f, 0.f, 0.f, 0.f};
-            stored_prev = true;
+            st1 = 8;
         }
-        // (6) record n + 4 into this record's buffer, once its reads are done
+        // (6) record n + 4 into this record's buffer once its reads are done,
+        // then the X ids of step n + 5
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
         issue_rec(next_off, next_nvec, n);
+        issue_xid(n + XID_AHEAD);
         __builtin_amdgcn_sched_barrier(0);
     }
     // the last DMAs land before the workgroup's LDS is released
@@ -1570,7 +1599,7 @@ int boo_pick_f(int K) {
 #define SPMM_BOO_FAR 2          // streaming tile data loaded this many tiles ahead
 #endif
 #ifndef SPMM_BOO_BLOB_DX
-#define SPMM_BOO_BLOB_DX 2      // X tiles of the record-stream kernel staged this many steps ahead
+#define SPMM_BOO_BLOB_DX 1      // X tiles of the record kernel staged this many steps ahead
 #endif
 
 // Full feature tiles in one launch, a partial last tile (K % 2F != 0) in a
@@ -1592,7 +1621,8 @@ int launch_boo_stream_a(const StreamArgs<T>& a, hipStream_t s) {
     if constexpr (std::is_same<T, float>::value && F == 32 && VEC == 4 && A32) {
         if (wg4 && full > 0 && a.blobs && a.blob_first) {  // full 64-feature tiles, every load a DMA
             const dim3 grid(round_up8(a.n_waves / 4), full, a.batch);
-            BlobArgs ba{a.rows, a.cols, a.K, a.batch, a.n_waves, a.blobs, a.blob_first, a.X, a.Y, a.P};
+            BlobArgs ba{a.rows, a.cols, a.K, a.batch, a.n_waves, a.blobs, a.blob_first, a.blob_xid, a.row_ids,
+                        a.X, a.Y, a.P};
             hipLaunchKernelGGL((boo_blob_kernel<SPMM_BOO_BLOB_DX>), grid, dim3(256), 0, s, ba, 0);
             const int rc = check_launch("boo_blob_kernel");
             if (rc || a.K % (2 * F) == 0) return rc;
@@ -1778,9 +1808,10 @@ int boo_matmul_t(const spmm_boo_desc* A, const void* Xv, void* Yv, int64_t batch
     a.X = X;
     a.Y = Y;
     a.P = static_cast<T*>(ws);
-    const bool recs = A->n_blob16 > 0 && A->blobs && A->blob_first;
+    const bool recs = A->n_blob16 > 0 && A->blobs && A->blob_first && A->blob_xid;
     a.blobs = recs ? static_cast<const uint32_t*>(A->blobs) : nullptr;
     a.blob_first = recs ? A->blob_first : nullptr;
+    a.blob_xid = recs ? A->blob_xid : nullptr;
     int rc = stream ? boo_dispatch<T>(a, s) : SPMM_OK;
     if (rc) return rc;
     if (A->n_crow > 0) {
@@ -1993,13 +2024,14 @@ int spmm_boo_stage_copy(const spmm_boo_stage* st, int32_t* tiles, uint16_t* tile
     return ok ? SPMM_OK : fail(SPMM_EINVAL, "null output array for a non-empty staging field");
 }
 
-int spmm_boo_stage_copy_blobs(const spmm_boo_stage* st, void* blobs, uint32_t* blob_first) {
+int spmm_boo_stage_copy_blobs(const spmm_boo_stage* st, void* blobs, uint32_t* blob_first, uint32_t* blob_xid) {
     if (!st) return fail(SPMM_EINVAL, "null staging handle");
     const spmm_stage::Staged& s = st->s;
     if (s.blobs.empty()) return SPMM_OK;
-    if (!blobs || !blob_first) return fail(SPMM_EINVAL, "null output array for the record stream");
+    if (!blobs || !blob_first || !blob_xid) return fail(SPMM_EINVAL, "null output array for the record stream");
     std::memcpy(blobs, s.blobs.data(), s.blobs.size() * 4);
     std::memcpy(blob_first, s.blob_first.data(), s.blob_first.size() * 4);
+    std::memcpy(blob_xid, s.blob_xid.data(), s.blob_xid.size() * 4);
     return SPMM_OK;
 }
 

@@ -171,7 +171,27 @@ def test_stream_dense_block_is_cut_between_rows():
     boo = S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32)
     st = check_stream(A, boo)
     tiles = st['tiles'].reshape(-1, 8)
-    assert len(tiles) == 8 and np.all(tiles[:, 1] & 0xff == 128)
+    # 96 entries per tile at most: 3 whole rows of 32, the last tile 2 rows
+    assert len(tiles) == 11 and np.all(tiles[:-1, 1] & 0xff == 96) and tiles[-1, 1] & 0xff == 64
+
+
+def test_stream_cuts_inside_a_row_longer_than_a_tile():
+    """Duplicate entries can give one row of one block more entries than a
+    tile holds; the row is cut inside, its parts in consecutive tiles of the
+    same item, and no tile exceeds 96 entries."""
+    n_dup = 250
+    rows = np.r_[np.zeros(n_dup, int), np.arange(1, 40)]
+    cols = np.r_[np.full(n_dup, 3), np.arange(1, 40) % 37]
+    vals = np.arange(1, rows.size + 1, dtype=np.float32)
+    order = np.lexsort((cols, rows))      # CSR built directly: the duplicates stay separate entries
+    A = sp.csr_matrix((vals[order], cols[order], np.r_[0, np.cumsum(np.bincount(rows, minlength=40))]),
+                      shape=(40, 40))
+    assert A.nnz == rows.size
+    boo = S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32)
+    for group in (1, 4):
+        st = check_stream(A, boo, group=group)
+        nnz = st['tiles'].reshape(-1, 8)[:, 1] & 0xff
+        assert nnz.max() <= 96 and nnz.sum() >= n_dup
 
 
 def test_stream_splits_heavy_items_and_long_rows():
@@ -361,17 +381,11 @@ def decode_records(st):
             w0 = int(h[0])
             d = {'nnz': w0 & 0xff, 'nr': (w0 >> 8) & 63, 'nc': (w0 >> 14) & 63, 'flags': (w0 >> 20) & 15,
                  'slot': int(np.int32(h[1])), 'next_off': int(h[2]), 'next_nvec': w0 >> 24,
-                 'base': int(h[3]), 'off': o, 'nvec': nv}
+                 'rbase': int(h[3]), 'off': o, 'nvec': nv}
             p = 16
-            if not d['flags'] & 8:
-                d['cid'] = rec[p:p + 32].view(np.int32).copy()
-                p += 32
             if d['nnz']:
                 d['rs'] = rec[p:p + 32].copy()
                 p += 32
-            if d['flags'] & 4:
-                d['rowid'] = rec[p:p + 128].view(np.int32).copy()
-                p += 128
             nnz = d['nnz']
             d['col'] = rec[p:p + nnz].copy()
             p += (nnz + 3) & ~3
@@ -383,16 +397,17 @@ def decode_records(st):
     return out
 
 
-@pytest.mark.parametrize('case', ['stencil', 'permuted', 'rmat', 'heavy'])
+@pytest.mark.parametrize('case', ['stencil', 'permuted', 'rmat', 'heavy', 'hem'])
 def test_record_stream_matches_tiles(case):
     """The record stream holds exactly the tiles of the tile stream: per wave
-    and step its entries, row starts, the X rows it stages (2 of the 8 DMA
-    instructions of the step's 32-column tile), the slice's row ids at an
-    item's end; each record's look-ahead link names the record 4 steps later
-    (the last one for the stream's final records)."""
+    and step its entries, row starts and the slice's rows (first row when
+    consecutive, else its offset into row_ids); the X-id stream names the X
+    rows each wave stages (2 of the 8 DMA instructions of the step's
+    32-column tile); each record's look-ahead link names the record 4 steps
+    later (the last one for the stream's final records)."""
     if case == 'stencil':
         A = M.stencil_27pt(16)
-    elif case == 'permuted':
+    elif case in ('permuted', 'hem'):
         A = M.permuted(M.stencil_27pt(12), seed=3)
     elif case == 'rmat':
         A = M.rmat(12, 8, seed=1)
@@ -400,21 +415,25 @@ def test_record_stream_matches_tiles(case):
         rng = np.random.default_rng(5)
         A = sp.random(96, 96, density=0.9, random_state=rng, format='csr', dtype=np.float32)
     A = sp.csr_matrix(A, dtype=np.float32)
-    boo = S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32)
+    boo = S.csr_to_boo(A, cluster='hem' if case == 'hem' else 'identity', target_nr=32, target_nc=32)
     host = _host(boo)
-    st = _core.boo_stage(host, 512 if case == 'heavy' else 4096, 256, 64, 4, 1.5)
+    st = _core.boo_stage(host, 512 if case == 'heavy' else 4096, 256, 64, 4, 0.0 if case == 'hem' else 1.5)
     if st['n_waves'] == 0:
         assert st['n_blob16'] == 0
         return
     assert st['n_blob16'] == len(st['blobs']) // 4 > 0
     tiles = st['tiles'].reshape(-1, 8)
     trs = st['tile_rs'].reshape(-1, 33)
+    xid = st['blob_xid'].reshape(-1, 8)
+    assert len(xid) == len(tiles)
     wt = st['wave_tiles']
     recs = decode_records(st)
+    first = st['blob_first'].reshape(-1, 8)
+    n_noncontig = 0
     for w in range(st['n_waves']):
         m = w % 4
         t0, t1 = wt[w], wt[w + 1]
-        assert len(recs[w]) == t1 - t0
+        assert len(recs[w]) == t1 - t0 and first[w][6] == t0
         for k, t in enumerate(range(t0, t1)):
             d = recs[w][k]
             eo, w1, co, ro, slot = (int(x) for x in tiles[t][:5])
@@ -428,21 +447,19 @@ def test_record_stream_matches_tiles(case):
             # the X rows this wave stages: column 2m + (j >> 2) + 8 (j & 3)
             cols = [min(2 * m + (j >> 2) + 8 * (j & 3), max(nc - 1, 0)) for j in range(8)]
             want = [st['tcols'][co + c] if nc else 0 for c in cols]
-            if d['flags'] & 8:
-                got = [d['base'] + min(2 * m + (j >> 2) + 8 * (j & 3), d['nc'] - 1) for j in range(8)]
+            assert list(xid[t]) == want
+            rows = host['row_ids'][ro:ro + nr]
+            if d['flags'] & 4:
+                assert nr > 0 and np.array_equal(rows, d['rbase'] + np.arange(nr))
             else:
-                got = list(d['cid'])
-            assert got == want
-            if (fl & 1) and slot < 0 and nr > 0:
-                assert d['flags'] & 4
-                assert np.array_equal(d['rowid'][:nr], host['row_ids'][ro:ro + nr])
-            else:
-                assert not d['flags'] & 4
+                n_noncontig += nr > 0
+                assert d['rbase'] == ro
+    if case == 'hem':
+        assert n_noncontig > 0          # HEM slices' rows are scattered: the row_ids path is staged
     # the 4-step links: past the stream's end they name its last record (the
     # kernel prefetches it again and never uses it); every record lies inside
     # the stream
     blobs16 = len(st['blobs']) // 4
-    first = st['blob_first'].reshape(-1, 8)
     for w in range(st['n_waves']):
         n = len(recs[w])
         for k in range(n):
