@@ -211,6 +211,20 @@ int spmm_boo_matmul(const spmm_boo_desc* A, spmm_dtype dtype,
                     const void* X, void* Y, int64_t batch, int64_t K,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/* Y = A X like spmm_boo_matmul, but allocating nothing and taking no
+ * workspace: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference.  The workspace lives in a fixed 64 MiB
+ * device array of the library (one per GPU, held until the process ends;
+ * its address is looked up once per device on the first call there).
+ * Returns SPMM_ENOMEM when spmm_boo_workspace_bytes exceeds 64 MiB (no work
+ * is enqueued).  Calls on one GPU share that array: calls that overlap on one
+ * GPU (different streams, or host threads) race and must be serialised by
+ * the caller.  Every byte of workspace a call reads it has written itself
+ * earlier in the same call, so no clearing is needed between calls. */
+int spmm_boo_matmul_noalloc(const spmm_boo_desc* A, spmm_dtype dtype,
+                            const void* X, void* Y, int64_t batch, int64_t K, void* stream);
+
 /* ---------------------------------------------------------------------------
  * PBR (packed block rows).  Arrays are those csr_to_pbr emits
  * (pbr_matrix/pbr_matrix.hpp:98-167): codes as the 64-bit bitset pattern,

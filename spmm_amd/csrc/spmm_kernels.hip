@@ -48,6 +48,7 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <mutex>
 #include <new>
 #include <type_traits>
 #include <string>
@@ -1911,6 +1912,44 @@ int check_shape(int64_t batch, int64_t K) {
     return SPMM_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Scratch of the allocation-free BOO entry point: a file-scope device array
+// (one copy per GPU, held until the process ends).  In host code `scratch`
+// names a host-side stand-in, not device memory: its device address comes
+// from hipGetSymbolAddress, once per device, with that device current.
+// ---------------------------------------------------------------------------
+
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)64 << 20;
+constexpr int NOALLOC_MAX_DEVICES = 64;
+
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[NOALLOC_MAX_DEVICES];
+
+// Device address of this GPU's scratch (the current device's).
+int scratch_for_current_device(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(SPMM_ELAUNCH, "hipGetDevice failed: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= NOALLOC_MAX_DEVICES) return fail(SPMM_EUNSUPPORTED, "device index %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return fail(SPMM_ELAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                        hipGetErrorString(e));
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return SPMM_OK;
+}
+
 }  // namespace
 
 // ===========================================================================
@@ -2055,6 +2094,26 @@ int spmm_boo_matmul(const spmm_boo_desc* A, spmm_dtype dtype, const void* X, voi
     if (dtype == SPMM_F32) return boo_matmul_t<float>(A, X, Y, batch, K, workspace, workspace_bytes, s);
     if (dtype == SPMM_F64) return boo_matmul_t<double>(A, X, Y, batch, K, workspace, workspace_bytes, s);
     return fail(SPMM_EINVAL, "unknown dtype %d", (int)dtype);
+}
+
+int spmm_boo_matmul_noalloc(const spmm_boo_desc* A, spmm_dtype dtype, const void* X, void* Y,
+                            int64_t batch, int64_t K, void* stream) {
+    if (!A) return fail(SPMM_EINVAL, "null BOO descriptor");
+    int rc = check_shape(batch, K);
+    if (rc) return rc;
+    if (dtype != SPMM_F32 && dtype != SPMM_F64) return fail(SPMM_EINVAL, "unknown dtype %d", (int)dtype);
+    const size_t need = spmm_boo_workspace_bytes(A, dtype, batch, K);
+    if (need > NOALLOC_SCRATCH_BYTES)
+        return fail(SPMM_ENOMEM,
+                    "spmm_boo_matmul_noalloc: this staging and shape need %zu bytes of workspace, more than its "
+                    "%zu-byte scratch; call spmm_boo_matmul with a workspace instead",
+                    need, NOALLOC_SCRATCH_BYTES);
+    void* ws = nullptr;
+    if (need > 0) {
+        rc = scratch_for_current_device(&ws);
+        if (rc) return rc;
+    }
+    return spmm_boo_matmul(A, dtype, X, Y, batch, K, ws, need > 0 ? NOALLOC_SCRATCH_BYTES : 0, stream);
 }
 
 int spmm_pbr_matmul(const spmm_pbr_desc* A, spmm_dtype dtype, const void* X, void* Y,
