@@ -61,6 +61,11 @@ def _tile_by_permutation(perm: np.ndarray, n: int, target: int) -> np.ndarray:
 
 
 def _relabel_consecutive(labels: np.ndarray) -> np.ndarray:
+    labels = np.asarray(labels)
+    if labels.size and labels[0] == 0:
+        d = np.diff(labels)
+        if np.all((d == 0) | (d == 1)):          # already 0, 1, ... in order (identity)
+            return labels.astype(np.int64, copy=False)
     _, inverse = np.unique(labels, return_inverse=True)
     return inverse.astype(np.int64, copy=False)
 
@@ -82,6 +87,17 @@ def _enforce_caps(labels: np.ndarray, row_nnz: np.ndarray, max_size: Optional[in
     sorted_labels = labels[order]
     starts = np.flatnonzero(np.r_[True, sorted_labels[1:] != sorted_labels[:-1]])
     bounds = np.r_[starts, sorted_labels.size]
+    if max_nnz is None:
+        # size cap only: each group is cut into runs of max_size members in
+        # member order, and the groups' runs are numbered one after another
+        # -- the loop below, without the loop
+        sizes = np.diff(bounds)
+        pos = np.arange(labels.size, dtype=np.int64) - np.repeat(starts, sizes)
+        runs = (sizes + max_size - 1) // max_size
+        base = np.r_[0, np.cumsum(runs)[:-1]]
+        out = np.empty_like(labels)
+        out[order] = np.repeat(base, sizes) + pos // max_size
+        return out
     out = np.empty_like(labels)
     nxt = 0
     for g in range(starts.size):

@@ -235,3 +235,19 @@ def test_hem_labels_equal_reference_vectors(case):
         r, c = C.cluster_axes(A, 'hem', kw['target'], kw['target'], kw.get('max_size'),
                               kw.get('max_size'), feasible_first=kw['feasible_first'])
         assert np.array_equal(r, axes[0]) and np.array_equal(c, axes[1])
+
+
+def test_size_cap_without_the_member_loop():
+    """_enforce_caps with only a size cap runs without the per-member loop;
+    it must give the loop's labels (the loop runs when an nnz cap is given:
+    an nnz cap nothing reaches makes it the size-cap loop)."""
+    from spmm_amd import clustering as C
+    rng = np.random.default_rng(0)
+    for trial in range(200):
+        n = int(rng.integers(0, 300))
+        lab = rng.integers(0, max(1, int(rng.integers(1, 40))), n)
+        if trial % 3 == 0:
+            lab = np.sort(lab)
+        nnz = rng.integers(0, 10, n)
+        cap = int(rng.integers(1, 12))
+        assert np.array_equal(C._enforce_caps(lab, nnz, cap, None), C._enforce_caps(lab, nnz, cap, 10 ** 12))
