@@ -1,18 +1,10 @@
 """Parity at BASELINE.json's full sizes for configs 3, 4 and 5.
 
-Configs 1 and 2 are checked against the whole fp64 product
-(test_gpu_boo.py, test_gpu_pbr_csr.py).  These three are 33-56 M nonzeros,
-so the host side keeps to checks that stay cheap at that size:
-
-* 65,536 seeded rows (6-12 % of the rows, spread over the whole matrix)
-  against the oracle's fp64 product, elementwise |Y - AX| <= 1e-5 (|A||X|)
-  (the tolerance of the path): a wrong value in any sampled row fails;
-* a column checksum over every row: sum_r Y[r, f] = ((1^T A) X)_f within
-  1e-5 ((1^T |A|) |X|)_f, the sum of the elementwise bounds.  That bound is
-  loose at this size: it catches gross errors anywhere (a pass that did not
-  run, 1 % of the rows zeroed) but not one wrong row, which the sample is
-  for;
-* bit-equal results on a second call (plain stores, no atomics).
+Configs 1 and 2 are checked in test_gpu_boo.py and test_gpu_pbr_csr.py.
+These three are 33-56 M nonzeros; every row of Y is compared with the
+oracle's fp64 product, computed in row blocks so the host's memory stays
+bounded: |Y - AX| <= 1e-5 (|A||X|) elementwise (the tolerance of the path).
+A second call must give bit-equal results (plain stores, no atomics).
 
 The matrices are the bench's own (spmm_amd/matrices.py, seeded).
 """
@@ -21,16 +13,16 @@ import functools
 
 import numpy as np
 import pytest
+import scipy.sparse as sp
 import torch
 
 import spmm_amd as S
-from oracle import oracle as O
 from spmm_amd import matrices as M
 
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-5
-N_SAMPLE = 65536
+BLOCK = 1 << 17     # rows per block of the fp64 product
 
 
 @functools.lru_cache(maxsize=1)
@@ -41,24 +33,34 @@ def _config(cfg):
 
 
 def _check_full(y, A, x):
-    y64 = y.double()
-    # column checksum over all rows
-    ones = np.ones(A.shape[0])
-    colsum = ones @ A                       # 1^T A, fp64 (A is scipy, fp32 values)
-    abscolsum = ones @ abs(A)
-    ref = torch.from_numpy(colsum.astype(np.float64) @ x.astype(np.float64))
-    bound = torch.from_numpy(abscolsum.astype(np.float64) @ np.abs(x).astype(np.float64))
-    got = y64.sum(0).cpu()
-    assert torch.all((got - ref).abs() <= TOL * bound), \
-        f'column checksum: max excess {((got - ref).abs() - TOL * bound).max().item():.3e}'
-    # sampled rows against the fp64 product
-    rows = np.sort(np.random.default_rng(7).choice(A.shape[0], N_SAMPLE, replace=False))
-    ratio, ok = O.within_bound(y[torch.from_numpy(rows).cuda()].cpu().numpy(), A[rows], x, TOL)
-    assert ok, f'sampled rows: max |err|/(|A||X|) = {ratio:.3e}'
+    """Every element of y against the fp64 product, block of rows by block."""
+    x64 = x.astype(np.float64)
+    absx = np.abs(x64)
+    # private fp64 copies of A (the caller's arrays are not touched)
+    A64 = sp.csr_matrix((A.data.astype(np.float64), A.indices.copy(), A.indptr.copy()), shape=A.shape)
+    Aabs = sp.csr_matrix((np.abs(A64.data), A64.indices, A64.indptr), shape=A.shape)
+    yh = y.cpu().numpy()
+    worst = 0.0
+    for r0 in range(0, A.shape[0], BLOCK):
+        r1 = min(A.shape[0], r0 + BLOCK)
+        ref = A64[r0:r1] @ x64
+        bound = Aabs[r0:r1] @ absx
+        err = np.abs(yh[r0:r1].astype(np.float64) - ref)
+        bad = err > TOL * bound
+        if bad.any():
+            r, f = np.argwhere(bad)[0]
+            raise AssertionError(f'row {r0 + r} feature {f}: |err| {err[r, f]:.3e} > {TOL} x {bound[r, f]:.3e}')
+        with np.errstate(divide='ignore', invalid='ignore'):
+            q = np.where(bound > 0, err / np.where(bound > 0, bound, 1), 0.0)
+        worst = max(worst, float(q.max()) if q.size else 0.0)
+    print(f'  every row within the bound; max |err| / (|A||X|) = {worst:.3e}', flush=True)
 
 
+# generating a config takes up to ~80 s on the host, the fp64 check ~15 s
+@pytest.mark.timeout(480)
 @pytest.mark.parametrize('cfg,fmt', [(3, 'pbr'), (4, 'boo'), (5, 'boo'), (5, 'pbr')])
 def test_full_size_config(cfg, fmt):
+    print(f'config {cfg} {fmt}: generating', flush=True)
     A, spec, x_np = _config(cfg)
     print(f'config {cfg} {fmt}: {A.shape} nnz={A.nnz} K={spec["K"]}', flush=True)
     if fmt == 'boo':
