@@ -11,6 +11,14 @@ Two artefacts, both next to this file:
 ``python spmm_amd/build.py`` rebuilds both (run by path: importing the package
 needs the libraries this script builds).  Nothing is JIT-compiled at import
 time: ``spmm_amd`` loads what is here and fails loudly when it is missing.
+
+Host-code sanitizers (CPU only; the GPU code is never built with them):
+
+* ``python spmm_amd/build.py core-san`` -- ``_core`` with AddressSanitizer and
+  UBSan (every UB check fatal) into ``_build/san/``;
+* ``python spmm_amd/build.py san-test [pytest args]`` -- builds it and runs
+  ``pytest -m "not gpu"`` with that module loaded in place of ``_core``
+  (``SPMM_AMD_CORE``) and the sanitizer runtimes preloaded into Python.
 """
 
 from __future__ import annotations
@@ -62,13 +70,45 @@ def build_hip():
     _run([_hipcc(), *HIPCC_FLAGS, f'-I{INCLUDE}', *srcs, '-o', HIP_LIB, '-ldl'])
 
 
-def build_core():
+def build_core(out=CORE_LIB, flags=CXX_FLAGS, rpath='$ORIGIN'):
     import pybind11
     src = CSRC / 'core.cpp'
     py_inc = sysconfig.get_paths()['include']
-    _run(['g++', *CXX_FLAGS, f'-I{INCLUDE}', f'-I{CSRC}', f'-I{pybind11.get_include()}',
-          f'-I{py_inc}', src, '-o', CORE_LIB, f'-L{HERE}', '-lspmm_amd',
-          "-Wl,-rpath,$ORIGIN"])
+    _run(['g++', *flags, f'-I{INCLUDE}', f'-I{CSRC}', f'-I{pybind11.get_include()}',
+          f'-I{py_inc}', src, '-o', out, f'-L{HERE}', '-lspmm_amd', f'-Wl,-rpath,{rpath}'])
+
+
+SAN_CORE = ROOT / '_build' / 'san' / CORE_LIB.name
+SAN_FLAGS = ['-O1', '-g', '-fno-omit-frame-pointer', '-fsanitize=address,undefined',
+             '-fno-sanitize-recover=all', *[f for f in CXX_FLAGS if f != '-O3']]
+
+
+def build_core_san():
+    SAN_CORE.parent.mkdir(parents=True, exist_ok=True)
+    build_core(SAN_CORE, SAN_FLAGS, str(HERE))
+
+
+def san_env():
+    runtimes = []
+    for lib in ('libasan.so', 'libubsan.so'):
+        path = subprocess.run(['g++', f'-print-file-name={lib}'], check=True, capture_output=True,
+                              text=True).stdout.strip()
+        runtimes.append(path)
+    env = dict(os.environ)
+    env.update(SPMM_AMD_CORE=str(SAN_CORE), LD_PRELOAD=' '.join(runtimes),
+               # Python and torch are not instrumented: their allocations are
+               # outside the checks, and their exit-time leaks are not ours
+               ASAN_OPTIONS='detect_leaks=0:alloc_dealloc_mismatch=0:abort_on_error=1',
+               UBSAN_OPTIONS='print_stacktrace=1:halt_on_error=1')
+    return env
+
+
+def san_test(args):
+    build_core_san()
+    cmd = [sys.executable, '-m', 'pytest', str(ROOT / 'tests'), '-q', '-m', 'not gpu', '-p',
+           'no:cacheprovider', *args]
+    print('+', ' '.join(cmd), flush=True)
+    sys.exit(subprocess.run(cmd, env=san_env(), cwd=ROOT).returncode)
 
 
 def build_all():
@@ -78,5 +118,7 @@ def build_all():
 
 if __name__ == '__main__':
     which = sys.argv[1:] or ['all']
+    if which[0] == 'san-test':
+        san_test(which[1:])
     for w in which:
-        {'all': build_all, 'hip': build_hip, 'core': build_core}[w]()
+        {'all': build_all, 'hip': build_hip, 'core': build_core, 'core-san': build_core_san}[w]()

@@ -381,6 +381,42 @@ def test_scaled_down_power_law_and_permuted_configs(which, monkeypatch):
     assert torch.equal(S.boo_matmul(boo, x), y)
 
 
+def _permuted_path(n, seed=3):
+    T = sp.diags([-np.ones(n - 1), 2 * np.ones(n), -np.ones(n - 1)], [-1, 0, 1], format='csr',
+                 dtype=np.float32)
+    p = np.random.default_rng(seed).permutation(n)
+    return T[p][:, p].tocsr()
+
+
+def _permuted_laplacian_2d(m, seed=4):
+    I = sp.identity(m, format='csr', dtype=np.float32)
+    L1 = sp.diags([-np.ones(m - 1), 2 * np.ones(m), -np.ones(m - 1)], [-1, 0, 1], format='csr',
+                  dtype=np.float32)
+    L = (sp.kron(L1, I) + sp.kron(I, L1)).tocsr()
+    p = np.random.default_rng(seed).permutation(L.shape[0])
+    return L[p][:, p].tocsr()
+
+
+@pytest.mark.parametrize('which', ['path_200000', 'laplacian_2d_448'])
+@pytest.mark.parametrize('K', [16, 64])
+def test_reordered_gather_rows(which, K, monkeypatch):
+    """Gather rows walked in breadth-first (Cuthill-McKee) order, not row
+    order: the stage reorders them when that keeps the X rows they read close.
+    The whole Y against the fp64 product, and a second call bit-equal."""
+    monkeypatch.setattr(SB, 'MIN_COL_REUSE', 1.5)
+    A = _permuted_path(200_000) if which == 'path_200000' else _permuted_laplacian_2d(448)
+    boo = S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32).to('cuda')
+    d = boo._gpu_meta.desc
+    n_short = d['n_crow'] - d['n_crow_long']
+    assert n_short > 0.9 * A.shape[0]
+    cid = boo._gpu_meta.stage.crow_id[:n_short].cpu().numpy()
+    assert not np.all(np.diff(cid) > 0), 'the stage kept row order: the reorder did not fire'
+    x = _x((1, A.shape[1], K)).cuda()
+    y = S.boo_matmul(boo, x)
+    check(y, A, x)
+    assert torch.equal(S.boo_matmul(boo, x), y)
+
+
 @pytest.mark.parametrize('K', [4, 32, 130])
 def test_long_gather_rows_in_chunks(K, monkeypatch):
     monkeypatch.setattr(SB, 'MIN_COL_REUSE', 1.5)
