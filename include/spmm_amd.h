@@ -7,9 +7,11 @@
  * `h_`.  The caller owns every buffer, including Y and the workspace; nothing
  * here allocates device memory.  All work is enqueued on `stream` (a
  * hipStream_t, NULL = the legacy default stream) and is asynchronous with
- * respect to the host.  Entry points keep no global state and are re-entrant;
- * concurrent calls on different streams are safe as long as they do not share
- * Y or workspace.
+ * respect to the host.  Entry points are re-entrant; concurrent calls on
+ * different streams are safe as long as they do not share Y or workspace.
+ * The only process-wide state is the PBR launch knob
+ * (spmm_pbr_set_slab_bytes) and the per-GPU scratch array of
+ * spmm_boo_matmul_noalloc.
  *
  * Every entry point returns an spmm_status; on failure spmm_last_error()
  * returns a thread-local message naming the failed check.
@@ -72,7 +74,7 @@ const char* spmm_version(void);
  *
  * The caller copies the arrays to the device and fills spmm_boo_desc.
  * Every row group is cut into 32-row slices; each slice's work becomes tiles
- * of <= 32 rows x <= 32 columns with <= 128 entries (block entries keep the
+ * of <= 32 rows x <= 32 columns with <= 96 entries (block entries keep the
  * block's row-major order; the slice's remainder rows with <= long_threshold
  * entries become tiles over their distinct columns; longer remainder rows are
  * listed in long_rows and summed by a split-row pass).  A slice heavier than
@@ -255,6 +257,17 @@ typedef struct spmm_pbr_desc {
 int spmm_pbr_matmul(const spmm_pbr_desc* A, spmm_dtype dtype,
                     const void* X, void* Y, int64_t batch, int64_t K, void* stream);
 
+/* Launch knob of the PBR multiply, in the manner of the reference's
+ * set_boo_feat_block / set_boo_rowseg_fpt (bindings/bindings_boo.cu:409-420):
+ * process-wide, read at each call.  When one batch's X is larger than
+ * `bytes` (0, the default: never), the stripe kernel runs its feature tiles
+ * one launch after another at the small tile width (64 float / 32 double
+ * features), so one tile's X columns can stay in the last-level cache while
+ * every stripe reads them; otherwise one launch covers every tile.  Results
+ * are the same either way. */
+int spmm_pbr_set_slab_bytes(int64_t bytes);
+int64_t spmm_pbr_get_slab_bytes(void);
+
 /* ---------------------------------------------------------------------------
  * Naive CSR baseline: Y[r][f] = sum_j val[j] * X[col[j]][f], one thread per
  * output element, plain stores (kernels/csr_kernels.cu:5-29 semantics).
@@ -262,6 +275,37 @@ int spmm_pbr_matmul(const spmm_pbr_desc* A, spmm_dtype dtype,
 int spmm_csr_naive(const void* indptr, const void* col_ind, const void* vals,
                    spmm_itype itype, spmm_dtype dtype, int64_t rows, int64_t cols,
                    const void* X, void* Y, int64_t K, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Launch introspection.  Replaces boo_rowseg_launch_info and
+ * boo_nnzflat_launch_info (kernels/boo_kernel.cu:710-797, bound at
+ * bindings/bindings_boo.cu:421-475): the kernel the reference's launcher
+ * would select, with registers, local bytes, static shared memory and
+ * resident blocks per SM from the runtime.  Here the multiply's own dispatch
+ * runs with every launch recorded instead of enqueued, so each entry is a
+ * kernel the same call of spmm_boo_matmul / spmm_pbr_matmul launches, in
+ * launch order, with the runtime's attributes of that instance
+ * (hipFuncGetAttributes) and its resident workgroups per CU at its block size
+ * (hipOccupancyMaxActiveBlocksPerMultiprocessor).  X and Y are used only for
+ * their alignment, which steers the dispatch (NULL: 16-byte aligned).  Up to
+ * cap entries are written; *n_out is the number of launches.  Errors are
+ * those of the multiply.  Needs a GPU (the runtime's attribute queries).
+ * ------------------------------------------------------------------------- */
+typedef struct spmm_launch_info {
+    const char* kernel;          /* kernel family name (static string) */
+    uint32_t grid[3];            /* workgroups in x, y, z */
+    uint32_t block;              /* threads per workgroup */
+    int32_t registers;           /* hipFuncAttributes.numRegs: VGPRs per lane */
+    int32_t scratch_bytes;       /* localSizeBytes: private (spill) bytes per lane */
+    int32_t lds_bytes;           /* sharedSizeBytes: static LDS per workgroup */
+    int32_t max_threads;         /* maxThreadsPerBlock (the launch bound) */
+    int32_t wgs_per_cu;          /* resident workgroups per CU at this block size */
+} spmm_launch_info;
+
+int spmm_boo_launch_info(const spmm_boo_desc* A, spmm_dtype dtype, const void* X, const void* Y,
+                         int64_t batch, int64_t K, spmm_launch_info* out, int32_t cap, int32_t* n_out);
+int spmm_pbr_launch_info(const spmm_pbr_desc* A, spmm_dtype dtype, const void* X, const void* Y,
+                         int64_t batch, int64_t K, spmm_launch_info* out, int32_t cap, int32_t* n_out);
 
 /* ---------------------------------------------------------------------------
  * Measurement adjuncts.

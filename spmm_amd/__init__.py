@@ -13,7 +13,7 @@ from ._native import core as _core  # noqa: F401  (loads the native extension)
 from .boo import (  # noqa: E402
     BOOInfo, BOOMatrix, BOOMatrixInt32Double, BOOMatrixInt32Float, BOOMatrixInt64Double,
     BOOMatrixInt64Float, BooNzOrder, BooSmallBlockPolicy, NZ_ORDERS, SMALL_BLOCK_POLICIES,
-    boo_arena_bytes, boo_info, boo_matmul, boo_to_csr, csr_to_boo,
+    boo_arena_bytes, boo_info, boo_launch_info, boo_matmul, boo_to_csr, csr_to_boo,
 )
 from .clustering import CLUSTER_METHODS, cluster_axes, cluster_axis  # noqa: E402
 from .csr import spdmm_csr_naive  # noqa: E402
@@ -21,8 +21,8 @@ from .pbr import (  # noqa: E402
     BlockFillStats, BlockStripeStats, DataOrder, PBRInfo, PBRMatrix, PBRMatrixInt32Double,
     PBRMatrixInt32Float, PBRMatrixInt64Double, PBRMatrixInt64Float, csr_to_pbr,
     pbr_batched_matmul_chunkcols_cuda, pbr_batched_matmul_cpu, pbr_batched_matmul_cuda,
-    pbr_batched_matmul_nnzflat_cuda, pbr_batched_matmul_variant_cuda, pbr_info, pbr_matmul,
-    pbr_to_csr,
+    get_pbr_slab_bytes, pbr_batched_matmul_nnzflat_cuda, pbr_batched_matmul_variant_cuda, pbr_info,
+    pbr_launch_info, pbr_matmul, pbr_to_csr, set_pbr_slab_bytes,
 )
 from .plan import BOOExecutionPlan, prepare_boo_cuda  # noqa: E402
 from .timed import BOOTimedSpMM, DirectSpMM, PBRTimedSpMM  # noqa: E402

@@ -529,11 +529,12 @@ def boo_arena_bytes(max_nr: int, max_nc: int, max_nnz_blk: int, p: int, scalar_b
 
 
 def _gfx950_lds_bytes(scalar_bytes: int) -> int:
-    """LDS per workgroup of the gfx950 tile-stream kernel (4 waves, one slice
-    each, sharing a 32-column X tile of 64 features).  float: the LDS-DMA
-    kernel's chunk-major tile, double-buffered, 8 serial-row sums per wave and
-    136 entries per wave.  Other types: the register-staged kernel's padded
-    tile (row stride 64 features + 32 bytes), the same per-wave arrays and a
+    """Offline estimate of the LDS per workgroup of the gfx950 tile-stream
+    kernel, for a matrix that is not staged on a GPU (a staged one reports
+    the runtime's figure, boo_launch_info).  float: the LDS-DMA kernel's
+    chunk-major tile, double-buffered, 8 serial-row sums per wave and 136
+    entries per wave.  Other types: the register-staged kernel's padded tile
+    (row stride 64 features + 32 bytes), the same per-wave arrays and a
     32-entry column table per wave."""
     entry = 8 if scalar_bytes <= 4 else 16    # {uint32 column, value}, aligned
     if scalar_bytes == 4:
@@ -542,11 +543,38 @@ def _gfx950_lds_bytes(scalar_bytes: int) -> int:
     return 2 * 32 * stride + 4 * 8 * stride + 4 * 136 * entry + 4 * 32 * 4
 
 
+def boo_launch_info(boo_mat, features: int, batch: int = 1, x: Optional[torch.Tensor] = None,
+                    dtype: Optional[torch.dtype] = None) -> list:
+    """The kernels ``boo_matmul(boo_mat, X)`` launches for ``batch`` x
+    ``features`` columns, in launch order, each with the runtime's attributes
+    of that kernel instance: ``registers_per_thread`` (VGPRs),
+    ``local_bytes_per_thread`` (scratch: spills), ``static_shared_bytes``
+    (LDS), ``max_threads_per_block`` and ``max_active_blocks_per_cu``
+    (resident workgroups per CU at its block size), plus ``grid`` and
+    ``threads``.  The multiply's own dispatch runs with every launch recorded
+    instead of enqueued, so the list is what the multiply launches.  Replaces
+    boo_rowseg_launch_info / boo_nnzflat_launch_info
+    (kernels/boo_kernel.cu:710-797, bindings/bindings_boo.cu:421-475).
+    ``x`` (optional) supplies the alignment that steers the dispatch;
+    ``dtype`` defaults to the matrix's scalar type."""
+    meta = boo_mat._gpu_meta
+    if meta is None:
+        raise RuntimeError("[boo_launch_info] the BOOMatrix is not on a GPU. Call .to('cuda') first.")
+    if dtype is None:
+        dtype = torch.float32 if np.dtype(boo_mat.scalar_dtype) == np.float32 else torch.float64
+    with torch.cuda.device(meta.nz_val.device):
+        xp = int(x.data_ptr()) if x is not None else 0
+        return core.boo_launch_info(meta.desc, _DTYPE_CODE[dtype], xp, 0, int(batch), int(features))
+
+
 def boo_info(boo_mat, p: int = 64, threads: int = 256, row_seg: bool = True) -> BOOInfo:
     """Structural summary derived from the built format.  ``arena_bytes`` and
-    the occupancy fields describe this library's gfx950 tile-stream kernel
-    (256-lane workgroups of 4 waves, LDS-bound count per CU), not the
-    reference's CUDA launch."""
+    the occupancy fields describe this library's gfx950 kernel, not the
+    reference's CUDA launch: for a matrix staged on a GPU, the runtime's
+    figures (LDS, resident workgroups per CU) of the first kernel a multiply
+    of ``p`` features launches (boo_launch_info); otherwise an offline
+    estimate for the tile-stream kernel (256-lane workgroups of 4 waves,
+    LDS-bound count per CU)."""
     scalar_bytes = np.dtype(boo_mat.scalar_dtype).itemsize
     row_grp_ptr = np.asarray(boo_mat.row_grp_ptr, dtype=np.int64)
     col_grp_ptr = np.asarray(boo_mat.col_grp_ptr, dtype=np.int64)
@@ -573,8 +601,15 @@ def boo_info(boo_mat, p: int = 64, threads: int = 256, row_seg: bool = True) -> 
     compressed = boo_mat.compressed_nnz()
     tail = boo_mat.tail_nnz()
     total = int(boo_mat.total_nnz)
-    arena = _gfx950_lds_bytes(scalar_bytes)
-    wgs = max(0, min(_LDS_PER_CU // arena, _MAX_WAVES_PER_CU // 4))
+    if boo_mat._gpu_meta is not None and int(boo_mat.rows) > 0 and int(boo_mat.cols) > 0:
+        first = boo_launch_info(boo_mat, p)[0]
+        arena = int(first['static_shared_bytes'])
+        wgs = int(first['max_active_blocks_per_cu'])
+        waves = wgs * -(-int(first['threads']) // _WAVE)
+    else:
+        arena = _gfx950_lds_bytes(scalar_bytes)
+        wgs = max(0, min(_LDS_PER_CU // arena, _MAX_WAVES_PER_CU // 4))
+        waves = 4 * wgs
     return BOOInfo(
         shape=(int(boo_mat.rows), int(boo_mat.cols)), total_nnz=total, compressed_nnz=compressed,
         remainder_nnz=boo_mat.remainder_nnz(), tail_nnz=tail,
@@ -588,4 +623,4 @@ def boo_info(boo_mat, p: int = 64, threads: int = 256, row_seg: bool = True) -> 
         x_loads=x_loads, y_writes=y_writes,
         arithmetic_intensity=compressed / x_loads if x_loads else 0.0,
         scalar_bytes=scalar_bytes, p=p, threads=threads, arena_bytes=arena, ctas_per_sm=wgs,
-        occupancy_pct=100.0 * 4 * wgs / _MAX_WAVES_PER_CU)
+        occupancy_pct=100.0 * waves / _MAX_WAVES_PER_CU)

@@ -7,11 +7,11 @@
 // several steps ahead without any dependent lookup, so every row group is cut
 // into 32-row slices and each slice's work into tiles:
 //
-//   * a tile is <= 32 rows x <= 32 columns with <= 128 entries, its entries
+//   * a tile is <= 32 rows x <= 32 columns with <= 96 entries, its entries
 //     sorted by local row (the block's row-major order is kept), each entry a
 //     value plus a one-byte local column, and a 33-entry row-start table;
 //   * a block contributes one tile per 32-column chunk of its column group
-//     (a chunk too full for 128 entries is cut between rows);
+//     (a chunk too full for 96 entries is cut between rows);
 //   * the slice's short remainder rows (<= long_threshold entries) contribute
 //     tiles over the sorted set of their distinct columns, 32 at a time;
 //     longer rows are listed for the split-row pass;

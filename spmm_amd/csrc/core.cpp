@@ -436,6 +436,46 @@ void pbr_matmul_gpu(const py::dict& d, int dtype, uintptr_t x, uintptr_t y, int6
                                  reinterpret_cast<void*>(y), batch, K, reinterpret_cast<void*>(stream)));
 }
 
+// ---- launch introspection: the kernels a multiply launches, with their
+// runtime attributes, as a list of dicts (one per launch, in order) ----
+
+py::list launch_list(const std::vector<spmm_launch_info>& v, int32_t n) {
+    py::list out;
+    for (int32_t i = 0; i < n; ++i) {
+        const spmm_launch_info& o = v[i];
+        py::dict d;
+        d["kernel"] = std::string(o.kernel);
+        d["grid"] = py::make_tuple(o.grid[0], o.grid[1], o.grid[2]);
+        d["threads"] = o.block;
+        d["registers_per_thread"] = o.registers;
+        d["local_bytes_per_thread"] = o.scratch_bytes;
+        d["static_shared_bytes"] = o.lds_bytes;
+        d["max_threads_per_block"] = o.max_threads;
+        d["max_active_blocks_per_cu"] = o.wgs_per_cu;
+        out.append(d);
+    }
+    return out;
+}
+
+template <typename Desc, typename Fn>
+py::list launch_info(const Desc& A, int dtype, uintptr_t x, uintptr_t y, int64_t batch, int64_t K, Fn fn) {
+    int32_t n = 0;
+    raise_status(fn(&A, (spmm_dtype)dtype, reinterpret_cast<const void*>(x), reinterpret_cast<const void*>(y),
+                    batch, K, nullptr, 0, &n));
+    std::vector<spmm_launch_info> v(n);
+    raise_status(fn(&A, (spmm_dtype)dtype, reinterpret_cast<const void*>(x), reinterpret_cast<const void*>(y),
+                    batch, K, v.data(), n, &n));
+    return launch_list(v, std::min<int32_t>(n, (int32_t)v.size()));
+}
+
+py::list boo_launch_info(const py::dict& d, int dtype, uintptr_t x, uintptr_t y, int64_t batch, int64_t K) {
+    return launch_info(boo_desc(d), dtype, x, y, batch, K, spmm_boo_launch_info);
+}
+
+py::list pbr_launch_info(const py::dict& d, int dtype, uintptr_t x, uintptr_t y, int64_t batch, int64_t K) {
+    return launch_info(pbr_desc(d), dtype, x, y, batch, K, spmm_pbr_launch_info);
+}
+
 // ---- measurement adjuncts: timers, C++-timed calls, the vendor SpMM plan ----
 // Handles cross into Python as integers; the Python classes own them.
 
@@ -529,6 +569,10 @@ PYBIND11_MODULE(_core, m) {
     m.def("boo_matmul_gpu", &boo_matmul_gpu);
     m.def("pbr_matmul_gpu", &pbr_matmul_gpu);
     m.def("csr_naive_gpu", &csr_naive_gpu);
+    m.def("boo_launch_info", &boo_launch_info);
+    m.def("pbr_set_slab_bytes", [](int64_t b) { raise_status(spmm_pbr_set_slab_bytes(b)); });
+    m.def("pbr_get_slab_bytes", []() { return spmm_pbr_get_slab_bytes(); });
+    m.def("pbr_launch_info", &pbr_launch_info);
     m.def("timer_create", &new_timer);
     m.def("timer_destroy", [](uintptr_t t) { spmm_timer_destroy(reinterpret_cast<spmm_timer*>(t)); });
     m.def("boo_matmul_gpu_timed", &boo_matmul_gpu_timed);

@@ -45,9 +45,11 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <cstring>
 #include <mutex>
 #include <new>
 #include <type_traits>
@@ -89,6 +91,27 @@ int check_launch(const char* what) {
         return fail(SPMM_ELAUNCH, "HIP launch of %s failed: %s", what, hipGetErrorString(e));
     }
     return SPMM_OK;
+}
+
+// Launch recorder.  While t_record is set (on this thread), launch() appends
+// the kernel, its grid and its block to it instead of launching: the
+// *_launch_info entry points run the multiply's own dispatch code this way,
+// so what they report is exactly what the multiply launches.
+struct LaunchRec {
+    const void* fn;
+    const char* name;
+    dim3 grid, block;
+};
+thread_local std::vector<LaunchRec>* t_record = nullptr;
+
+template <typename... P, typename... Args>
+int launch(const char* name, void (*kern)(P...), dim3 grid, dim3 block, hipStream_t s, Args&&... args) {
+    if (t_record) {
+        t_record->push_back({reinterpret_cast<const void*>(kern), name, grid, block});
+        return SPMM_OK;
+    }
+    hipLaunchKernelGGL(kern, grid, block, 0, s, std::forward<Args>(args)...);
+    return check_launch(name);
 }
 
 // ---------------------------------------------------------------------------
@@ -240,6 +263,16 @@ __device__ __forceinline__ int opaque_copy(int v) {
     int r;
     asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "v"(v));
     return r;
+}
+
+// A uniform pointer the compiler cannot trace back to the kernel argument it
+// was read from.  Selecting between two such fields (Y or a partial slot)
+// otherwise becomes a load through a selected field address, which keeps a
+// private copy of the whole argument struct in scratch.
+template <typename P>
+__device__ __forceinline__ P* opaque_ptr(P* p) {
+    asm volatile("" : "+s"(p));
+    return p;
 }
 
 
@@ -419,8 +452,8 @@ __device__ __forceinline__ void st_store(const StreamArgs<T>& a, const T (&acc)[
     const int lr = lane >> 1;
     const int K = a.K;
     if (lr < nrow) {
-        T* out = slot < 0 ? a.Y + ((size_t)b * a.rows + row) * K + fbase + h * VEC
-                          : a.P + (((size_t)slot * a.batch + b) * ST_ROWS + lr) * K + fbase + h * VEC;
+        T* out = slot < 0 ? opaque_ptr(a.Y) + ((size_t)b * a.rows + row) * K + fbase + h * VEC
+                          : opaque_ptr(a.P) + (((size_t)slot * a.batch + b) * ST_ROWS + lr) * K + fbase + h * VEC;
 #pragma unroll
         for (int q = 0; q < G::NQ; ++q)
             if (FULL || fbase + (2 * q + h) * VEC < K) store_vec<T, VEC>(out + 2 * q * VEC, acc[q]);
@@ -463,8 +496,11 @@ __device__ __forceinline__ void group_sync() {
 // item's tiles and stores them once, at the item's last tile (to Y, or to a
 // partial slot of a split item).  Steps past the end of the stream load its
 // last tile (the data is never used) and store nothing.
+// fp64 with 16 features per lane: 2 waves per SIMD, room for the 64
+// accumulators and the X staging registers without spilling.
 template <typename T, int F, int VEC, int D, int DF, int WG, bool FULL, bool A32>
-__global__ void __launch_bounds__(64 * WG, 4) boo_stream_kernel(StreamArgs<T> a, int kt0) {
+__global__ void __launch_bounds__(64 * WG, sizeof(T) == 8 && F >= 16 ? 2 : 4) boo_stream_kernel(StreamArgs<T> a,
+                                                                                                  int kt0) {
     typedef BooGeom<T, F, VEC> G;
     constexpr int NW = G::NST / WG;   // X staging instructions per wave
     static_assert(G::NST % WG == 0, "X tile does not split over the workgroup");
@@ -615,11 +651,18 @@ __global__ void __launch_bounds__(64 * WG, 4) boo_stream_kernel(StreamArgs<T> a,
 // chunks 2m+h of a column at one base plus 32-byte immediates.
 // ---------------------------------------------------------------------------
 
+#ifndef SPMM_BOO_DMA_HALVES
+#define SPMM_BOO_DMA_HALVES 1   // parts an entry's X row is read in by the LDS-DMA kernel's walk
+#endif
+#ifndef SPMM_BOO_DMA_OCC
+#define SPMM_BOO_DMA_OCC 4      // waves per SIMD the LDS-DMA kernel is compiled for
+#endif
 constexpr int DMA_BLK = 1056;  // bytes between DMA instruction blocks (1 KiB + 32)
+template <int WG>
 struct StDmaLds {
     float tile[2][8 * DMA_BLK / 4];
-    float syn[8 * DMA_BLK / 4];                 // wave w's serial rows: columns 8w .. 8w+7
-    NzEntry<float> nzp[4][ST_ENT + ST_SYN];
+    float syn[WG * ST_SYN * 64];                // wave w's serial row k: 256-byte row ST_SYN w + k
+    NzEntry<float> nzp[WG][ST_ENT + ST_SYN];
     int spare[4];                               // the row pass reads one entry past its range
 };
 
@@ -650,19 +693,26 @@ __device__ __forceinline__ void dma_row(float (&acc)[8][4], int j, int e, const 
         const NzEntry<float> nxt = nzp[j + 1];
         __builtin_amdgcn_sched_barrier(0);
         const float* xr = (const float*)(lds_char*)(tb + ent.col);
-        float x[8][4];
+        // the row's 32 features in SPMM_BOO_DMA_HALVES parts, each read and
+        // used before the next is read (fewer registers in flight)
+        constexpr int QP = 8 / SPMM_BOO_DMA_HALVES;
 #pragma unroll
-        for (int q = 0; q < 8; ++q) load_vec<float, 4>(xr + q * 8, x[q]);
+        for (int p = 0; p < SPMM_BOO_DMA_HALVES; ++p) {
+            float x[QP][4];
 #pragma unroll
-        for (int q = 0; q < 8; ++q)
+            for (int q = 0; q < QP; ++q) load_vec<float, 4>(xr + (p * QP + q) * 8, x[q]);
 #pragma unroll
-            for (int u = 0; u < 4; ++u) acc[q][u] += ent.val * x[q][u];
+            for (int q = 0; q < QP; ++q)
+#pragma unroll
+                for (int u = 0; u < 4; ++u) acc[p * QP + q][u] += ent.val * x[q][u];
+            if (p + 1 < SPMM_BOO_DMA_HALVES) __builtin_amdgcn_sched_barrier(0);
+        }
         ent = nxt;
     }
 }
 
 // st_serial for the DMA tile: lane f takes feature f; busy row k's
-// sums become column 8 wv + k of the shared syn tile.
+// sums become row ST_SYN wv + k of the syn rows (256 bytes each).
 __device__ __forceinline__ void dma_serial(uint64_t busy, int& rs0, int& rs1, NzEntry<float>* nzp,
                                            const float* tile, float* syn, int wv) {
     const int lane = threadIdx.x & 63;
@@ -684,7 +734,7 @@ __device__ __forceinline__ void dma_serial(uint64_t busy, int& rs0, int& rs1, Nz
             const NzEntry<float> a0 = nzp[j];
             s0 += a0.val * xc[a0.col >> 2];
         }
-        const uint32_t col = dma_col_off(8 * wv + k);
+        const uint32_t col = (uint32_t)(ST_SYN * wv + k) * 256u;
         syn[fo + (col >> 2)] = s0 + s1;
         if (lane == 0) nzp[ST_ENT + k] = NzEntry<float>{col, 1.f};
         if ((lane & ~1) == l2) {
@@ -694,11 +744,15 @@ __device__ __forceinline__ void dma_serial(uint64_t busy, int& rs0, int& rs1, Nz
     }
 }
 
-template <int DF>
-__global__ void __launch_bounds__(256, 4) boo_stream_dma_kernel(StreamArgs<float> a, int kt0) {
-    constexpr int D = 1, WG = 4;
+// WG waves (2 or 4) share each X tile: the tile's 8 DMA instructions are
+// split 8/WG per wave.
+template <int DF, int WG>
+__global__ void __launch_bounds__(64 * WG, SPMM_BOO_DMA_OCC) boo_stream_dma_kernel(StreamArgs<float> a, int kt0) {
+    constexpr int D = 1;
+    constexpr int NI = 8 / WG;  // DMA instructions per wave and tile
     static_assert(DF > D && ST_WORDS * (DF + D) <= 64, "bad prefetch depth");
-    __shared__ __attribute__((aligned(16))) StDmaLds L;
+    static_assert(WG == 2 || WG == 4, "the X tile splits over 2 or 4 waves");
+    __shared__ __attribute__((aligned(16))) StDmaLds<WG> L;
     const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int w = xcd_remap(blockIdx.x, gridDim.x) * WG + wv;
     if (w >= a.n_waves) return;  // uniform per workgroup: n_waves is a multiple of WG
@@ -714,18 +768,31 @@ __global__ void __launch_bounds__(256, 4) boo_stream_dma_kernel(StreamArgs<float
     auto cl = [tl](int t) { return min(t, tl); };
     NzEntry<float>* nzp = L.nzp[wv];
     const uint32_t rowb = (uint32_t)a.K * 4u;
-    // this wave's DMA instructions I = 2wv, 2wv+1 stage columns I + 8 (lane / 16),
-    // chunk lane % 16; a lane loads the column id of one of its two columns
-    // (scol) and takes the other from its neighbour lane ^ 1
-    const int scol = 2 * wv + 8 * (lane >> 4) + (lane & 1);
+    // this wave's DMA instructions I = NI wv + k (k < NI) stage columns
+    // I + 8 (lane / 16), chunk lane % 16.  A lane loads the column id of one
+    // of its NI columns (scol) and takes the others from the lanes next to it:
+    // NI = 2, from lane ^ 1; NI = 4, by broadcast inside its group of four.
+    const int scol = NI * wv + 8 * (lane >> 4) + (lane & (NI - 1));
     const uint32_t lane_off = (uint32_t)fbase * 4u + (uint32_t)(lane & 15) * 16u;
     const bool odd = (lane & 1) != 0;
     auto issue_dma = [&](int cid, int buf) {
-        const int oth = __builtin_amdgcn_mov_dpp(cid, 0xB1, 0xF, 0xF, false);  // lane ^ 1
-        const uint32_t c0 = (uint32_t)(odd ? oth : cid), c1 = (uint32_t)(odd ? cid : oth);
-        const uint32_t l0 = lds_u32(&L.tile[buf][0]) + (uint32_t)(2 * wv) * (uint32_t)DMA_BLK;
-        dma16(Xb, __umul24(c0, rowb) + lane_off, l0);
-        dma16(Xb, __umul24(c1, rowb) + lane_off, l0 + (uint32_t)DMA_BLK);
+        const uint32_t l0 = lds_u32(&L.tile[buf][0]) + (uint32_t)(NI * wv) * (uint32_t)DMA_BLK;
+        if constexpr (NI == 2) {
+            const int oth = __builtin_amdgcn_mov_dpp(cid, 0xB1, 0xF, 0xF, false);  // lane ^ 1
+            const uint32_t c0 = (uint32_t)(odd ? oth : cid), c1 = (uint32_t)(odd ? cid : oth);
+            dma16(Xb, __umul24(c0, rowb) + lane_off, l0);
+            dma16(Xb, __umul24(c1, rowb) + lane_off, l0 + (uint32_t)DMA_BLK);
+        } else {
+            // quad_perm(k, k, k, k): every lane of a group of four takes lane k's id
+            const uint32_t c0 = (uint32_t)__builtin_amdgcn_mov_dpp(cid, 0x00, 0xF, 0xF, false);
+            const uint32_t c1 = (uint32_t)__builtin_amdgcn_mov_dpp(cid, 0x55, 0xF, 0xF, false);
+            const uint32_t c2 = (uint32_t)__builtin_amdgcn_mov_dpp(cid, 0xAA, 0xF, 0xF, false);
+            const uint32_t c3 = (uint32_t)__builtin_amdgcn_mov_dpp(cid, 0xFF, 0xF, 0xF, false);
+            dma16(Xb, __umul24(c0, rowb) + lane_off, l0);
+            dma16(Xb, __umul24(c1, rowb) + lane_off, l0 + (uint32_t)DMA_BLK);
+            dma16(Xb, __umul24(c2, rowb) + lane_off, l0 + 2u * (uint32_t)DMA_BLK);
+            dma16(Xb, __umul24(c3, rowb) + lane_off, l0 + 3u * (uint32_t)DMA_BLK);
+        }
     };
 
     StFar<float> fr[DF];
@@ -1342,6 +1409,7 @@ template <typename T, typename I>
 struct PbrArgs {
     long long rows, cols;
     int K, n_stripes, long_threshold;
+    int kt0;                   // first feature tile of this launch
     const int64_t* codes;
     const I* coords;
     const I* offsets;
@@ -1357,26 +1425,37 @@ struct PbrArgs {
 // BR x BR blocks.  LPR = 64/BR lanes per stripe row; lane l of a row owns the
 // VEC-chunks q*LPR + l of the tile (q < NQ), so a row's lanes read one
 // contiguous run per instruction.
+// 8x8 blocks put two stripe rows in each 16-lane group of an LDS read.  A
+// row's LPR lanes read LPR * VEC * sizeof(T) = 128 contiguous bytes per chunk
+// q (32 banks); rows r and r+1 read random columns.  With the row stride a
+// multiple of 256 bytes and odd rows walking their chunks in the order q ^ 1
+// (SWAP), the two rows of a group always read opposite halves of the 64
+// banks, so the walk is free of bank conflicts whatever the columns.
+// Otherwise the stride is padded by 32 bytes.
 template <typename T, int BR, int KT, int VEC>
 struct PbrGeom {
     static constexpr int LPR = 64 / BR;
     static constexpr int F = KT / LPR;
     static constexpr int NQ = F / VEC;
     static constexpr int CHUNKS = KT / VEC;
-    static constexpr int STRIDE = KT + 32 / (int)sizeof(T);  // LDS row stride (elements), padded 32 B
+    static constexpr bool SWAP = BR == 8 && NQ % 2 == 0 && LPR * VEC * (int)sizeof(T) == 128 &&
+                                 (KT * (int)sizeof(T)) % 256 == 0;
+    static constexpr int STRIDE = SWAP ? KT : KT + 32 / (int)sizeof(T);  // LDS row stride (elements)
     static constexpr int STAGE_ITERS = (BR * CHUNKS + 63) / 64;
     static_assert(F % VEC == 0 && NQ >= 1, "bad PBR tile");
 };
 
-// One wave per stripe and feature tile, software-pipelined one block ahead:
-// while block n is walked from LDS, the X rows of block n+1 and the value of
-// its bit (r, c) -- one per lane -- are in flight into registers, and the
-// metadata of block n+2 behind them.  Every step issues the same loads (the
-// next block is clamped to the stripe's last), so no step waits on a load it
-// issued itself.  Lane (r, l) owns row r of the stripe and the VEC-chunks
+// One wave per stripe and feature tile, software-pipelined PD blocks ahead:
+// while block n is walked from LDS, the X rows of blocks n+1 .. n+PD and the
+// values of their bit (r, c) -- one per lane -- are in flight into
+// registers, and the metadata of block n+PD+1 behind them.  Every step issues
+// the same loads (blocks past the stripe's end are clamped to its last), so
+// no step waits on a load it issued itself, and a wave keeps PD blocks of X
+// in flight (small feature tiles: several, so the many short X reads of a
+// feature tile keep the memory system busy).  Lane (r, l) owns row r of the stripe and the VEC-chunks
 // q*LPR + l of the tile; it walks its row's set bits with ctz, reading the
 // bit's value and its X row slice from LDS.  Dense blocks are never formed.
-template <typename T, typename I, int BR, int KT, int VEC, bool FULL, bool A32>
+template <typename T, typename I, int BR, int KT, int VEC, int PD, bool FULL, bool A32>
 __device__ __forceinline__ void pbr_stripe_body(const PbrArgs<T, I>& a, int stripe, int kt, int b,
                                                 T* tiles, T* vals) {
     typedef PbrGeom<T, BR, KT, VEC> G;
@@ -1384,6 +1463,9 @@ __device__ __forceinline__ void pbr_stripe_body(const PbrArgs<T, I>& a, int stri
     const int lane = threadIdx.x;
     const int r = lane / G::LPR;
     const int l = lane % G::LPR;
+    // acc[q] of this lane holds feature chunk q ^ par (chunk order of SWAP)
+    const int par = G::SWAP ? (r & 1) : 0;
+    auto fofs = [&](int q) { return ((q ^ par) * G::LPR + l) * VEC; };  // chunk's first feature in the tile
     const long long row = (long long)stripe * BR + r;
     const bool active = row < a.rows;
     const int K = a.K;
@@ -1435,61 +1517,88 @@ __device__ __forceinline__ void pbr_stripe_body(const PbrArgs<T, I>& a, int stri
             const int rank = __popcll(code & ((1ull << (lane & 63)) - 1ull));
             return set ? a.data[off + rank] : T(0);
         };
-        uint64_t code_n = (uint64_t)a.codes[p0];
-        long long col_n = (long long)a.coords[2 * (size_t)p0 + 1];
-        long long off_n = (long long)a.offsets[p0];
-        T xr[G::STAGE_ITERS][VEC];
-        load_x(xr, col_n);
-        T vv = load_v(code_n, off_n);
-        const int q1 = min(p0 + 1, plast);
-        uint64_t code_f = (uint64_t)a.codes[q1];
-        long long col_f = (long long)a.coords[2 * (size_t)q1 + 1];
-        long long off_f = (long long)a.offsets[q1];
+        // Block metadata, lane-held: lane i holds code, column and value
+        // offset of block chunk + i (clamped to the stripe's last), one
+        // coalesced load per 64 blocks; each step reads its block's with
+        // readlane, so no step waits on a metadata load.
+        int chunk = p0;
+        uint64_t mcode;
+        long long mcol, moff;
+        auto meta_load = [&]() {
+            const int q = min(chunk + lane, plast);
+            mcode = (uint64_t)a.codes[q];
+            mcol = (long long)a.coords[2 * (size_t)q + 1];
+            moff = (long long)a.offsets[q];
+        };
+        auto rl64 = [](uint64_t v, int j) {
+            const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)v, j);
+            const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), j);
+            return ((uint64_t)hi << 32) | lo;
+        };
+        meta_load();
+        // The ring: slot s holds the X rows, the lane's bit value and the
+        // code of the block PD steps ahead of the one it is walking next.
+        T xr[PD][G::STAGE_ITERS][VEC];
+        T vv[PD];
+        uint64_t cd[PD];
+#pragma unroll
+        for (int s = 0; s < PD; ++s) {
+            cd[s] = rl64(mcode, s);
+            load_x(xr[s], (long long)rl64((uint64_t)mcol, s));
+            vv[s] = load_v(cd[s], (long long)rl64((uint64_t)moff, s));
+        }
         rem_prefetch();
-        for (int blk = p0, n = 0; blk < p1; ++blk, ++n) {
-            T* tile = tiles + (n & 1) * (BR * G::STRIDE);
-            T* vb = vals + (n & 1) * 64;
-            const uint64_t code = code_n;
-            // (1) block blk's X rows and values to LDS
+        for (int base = p0; base < p1; base += PD) {
 #pragma unroll
-            for (int m = 0; m < G::STAGE_ITERS; ++m) {
-                const int idx = m * 64 + lane;
-                const int c = idx / G::CHUNKS;
-                const int ch = idx % G::CHUNKS;
-                if (c < BR && (FULL || fbase + ch * VEC < K)) store_vec<T, VEC>(tile + c * G::STRIDE + ch * VEC, xr[m]);
-            }
-            vb[lane] = vv;
-            wave_lds_fence();
-            // (2) loads for block blk+1, metadata of block blk+2
-            code_n = code_f;
-            col_n = col_f;
-            off_n = off_f;
-            load_x(xr, col_n);
-            vv = load_v(code_n, off_n);
-            const int q2 = min(blk + 2, plast);
-            code_f = (uint64_t)a.codes[q2];
-            col_f = (long long)a.coords[2 * (size_t)q2 + 1];
-            off_f = (long long)a.offsets[q2];
-            // (3) walk block blk
-            if (active) {
-                uint32_t rb = (uint32_t)((code >> (BR * r)) & rowbits);
-                while (rb) {
-                    const int c = __builtin_ctz(rb);
-                    rb &= rb - 1u;
-                    const T v = vb[r * BR + c];
-                    const T* xrow = tile + c * G::STRIDE + l * VEC;
+            for (int s = 0; s < PD; ++s) {
+                const int blk = base + s;
+                if (blk >= p1) break;  // uniform
+                T* tile = tiles + ((blk - p0) & 1) * (BR * G::STRIDE);
+                T* vb = vals + ((blk - p0) & 1) * 64;
+                const uint64_t code = cd[s];
+                // (1) block blk's X rows and values to LDS
 #pragma unroll
-                    for (int q = 0; q < G::NQ; ++q) {
-                        if (FULL || fbase + (q * G::LPR + l) * VEC < K) {
-                            T x[VEC];
-                            load_vec<T, VEC>(xrow + q * G::LPR * VEC, x);
+                for (int m = 0; m < G::STAGE_ITERS; ++m) {
+                    const int idx = m * 64 + lane;
+                    const int c = idx / G::CHUNKS;
+                    const int ch = idx % G::CHUNKS;
+                    if (c < BR && (FULL || fbase + ch * VEC < K))
+                        store_vec<T, VEC>(tile + c * G::STRIDE + ch * VEC, xr[s][m]);
+                }
+                vb[lane] = vv[s];
+                wave_lds_fence();
+                // (2) loads of block blk+PD (clamped to the stripe's last)
+                // into the freed slot
+                int jn = blk + PD - chunk;
+                if (jn >= 64) {  // uniform; once per 64 blocks
+                    chunk += 64;
+                    jn -= 64;
+                    meta_load();
+                }
+                cd[s] = rl64(mcode, jn);
+                load_x(xr[s], (long long)rl64((uint64_t)mcol, jn));
+                vv[s] = load_v(cd[s], (long long)rl64((uint64_t)moff, jn));
+                // (3) walk block blk
+                if (active) {
+                    uint32_t rb = (uint32_t)((code >> (BR * r)) & rowbits);
+                    while (rb) {
+                        const int c = __builtin_ctz(rb);
+                        rb &= rb - 1u;
+                        const T v = vb[r * BR + c];
+                        const T* xrow = tile + c * G::STRIDE;
 #pragma unroll
-                            for (int u = 0; u < VEC; ++u) acc[q][u] += v * x[u];
+                        for (int q = 0; q < G::NQ; ++q) {
+                            if (FULL || fbase + fofs(q) < K) {
+                                T x[VEC];
+                                load_vec<T, VEC>(xrow + fofs(q), x);
+#pragma unroll
+                                for (int u = 0; u < VEC; ++u) acc[q][u] += v * x[u];
+                            }
                         }
                     }
                 }
+                wave_lds_fence();
             }
-            wave_lds_fence();
         }
     } else {
         rem_prefetch();
@@ -1507,7 +1616,7 @@ __device__ __forceinline__ void pbr_stripe_body(const PbrArgs<T, I>& a, int stri
                 const long long cu = rc[u] >= 0 ? (long long)rc[u] : 0;
 #pragma unroll
                 for (int q = 0; q < G::NQ; ++q) {
-                    const int fq = fbase + (q * G::LPR + l) * VEC;
+                    const int fq = fbase + fofs(q);
                     load_vec<T, VEC>(x_at<T, A32>(Xb, cu, K, FULL ? fq : min(fq, K - VEC)), xj[u][q]);
                 }
             }
@@ -1519,32 +1628,32 @@ __device__ __forceinline__ void pbr_stripe_body(const PbrArgs<T, I>& a, int stri
             for (int u = 0; u < RU; ++u)
 #pragma unroll
                 for (int q = 0; q < G::NQ; ++q)
-                    if (FULL || fbase + (q * G::LPR + l) * VEC < K)
+                    if (FULL || fbase + fofs(q) < K)
 #pragma unroll
                         for (int e = 0; e < VEC; ++e) acc[q][e] += vj[u] * xj[u][q][e];
         }
     }
     if (!active) return;
-    T* out = a.Y + ((size_t)b * a.rows + row) * K + fbase + l * VEC;
+    T* out = a.Y + ((size_t)b * a.rows + row) * K + fbase;
 #pragma unroll
     for (int q = 0; q < G::NQ; ++q) {
-        if (FULL || fbase + (q * G::LPR + l) * VEC < K) store_vec<T, VEC>(out + q * G::LPR * VEC, acc[q]);
+        if (FULL || fbase + fofs(q) < K) store_vec<T, VEC>(out + fofs(q), acc[q]);
     }
 }
 
-template <typename T, typename I, int BR, int KT, int VEC, bool A32>
+template <typename T, typename I, int BR, int KT, int VEC, int PD, bool A32>
 __global__ void __launch_bounds__(64) pbr_stripe_kernel(PbrArgs<T, I> a) {
     typedef PbrGeom<T, BR, KT, VEC> G;
     __shared__ __attribute__((aligned(16))) T tiles[2 * BR * G::STRIDE];
     __shared__ __attribute__((aligned(16))) T vals[2 * 64];
     const int stripe = xcd_remap(blockIdx.x, gridDim.x);
     if (stripe >= a.n_stripes) return;
-    const int kt = blockIdx.y;
+    const int kt = a.kt0 + (int)blockIdx.y;
     const int b = blockIdx.z;
     if ((kt + 1) * KT <= a.K) {
-        pbr_stripe_body<T, I, BR, KT, VEC, true, A32>(a, stripe, kt, b, tiles, vals);
+        pbr_stripe_body<T, I, BR, KT, VEC, PD, true, A32>(a, stripe, kt, b, tiles, vals);
     } else {
-        pbr_stripe_body<T, I, BR, KT, VEC, false, A32>(a, stripe, kt, b, tiles, vals);
+        pbr_stripe_body<T, I, BR, KT, VEC, PD, false, A32>(a, stripe, kt, b, tiles, vals);
     }
 }
 
@@ -1616,25 +1725,25 @@ int launch_boo_stream_a(const StreamArgs<T>& a, hipStream_t s) {
     const int full = a.K / (2 * F);
     auto go = [&](auto kern, int wg, int ny, int kt) {
         const dim3 grid(round_up8(a.n_waves / wg), ny, a.batch);
-        hipLaunchKernelGGL(kern, grid, dim3(64 * wg), 0, s, a, kt);
-        return check_launch("boo_stream_kernel");
+        return launch("boo_stream_kernel", kern, grid, dim3(64 * wg), s, a, kt);
     };
     if constexpr (std::is_same<T, float>::value && F == 32 && VEC == 4 && A32) {
         if (wg4 && full > 0 && a.blobs && a.blob_first) {  // full 64-feature tiles, every load a DMA
             const dim3 grid(round_up8(a.n_waves / 4), full, a.batch);
             BlobArgs ba{a.rows, a.cols, a.K, a.batch, a.n_waves, a.blobs, a.blob_first, a.blob_xid, a.row_ids,
                         a.X, a.Y, a.P};
-            hipLaunchKernelGGL((boo_blob_kernel<SPMM_BOO_BLOB_DX>), grid, dim3(256), 0, s, ba, 0);
-            const int rc = check_launch("boo_blob_kernel");
+            const int rc = launch("boo_blob_kernel", boo_blob_kernel<SPMM_BOO_BLOB_DX>, grid, dim3(256), s, ba, 0);
             if (rc || a.K % (2 * F) == 0) return rc;
             return go(boo_stream_kernel<T, F, VEC, D, DF, 4, false, A32>, 4, 1, full);
         }
-        if (wg4 && full > 0) {  // full 64-feature tiles: X staged by LDS DMA
-            const dim3 grid(round_up8(a.n_waves / 4), full, a.batch);
-            hipLaunchKernelGGL((boo_stream_dma_kernel<DF>), grid, dim3(256), 0, s, a, 0);
-            const int rc = check_launch("boo_stream_dma_kernel");
+        if ((wg4 || a.group == 2) && full > 0) {  // full 64-feature tiles: X staged by LDS DMA
+            const int wg = wg4 ? 4 : 2;
+            const dim3 grid(round_up8(a.n_waves / wg), full, a.batch);
+            const int rc = wg4 ? launch("boo_stream_dma_kernel", boo_stream_dma_kernel<DF, 4>, grid, dim3(256), s, a, 0)
+                               : launch("boo_stream_dma_kernel", boo_stream_dma_kernel<DF, 2>, grid, dim3(128), s, a, 0);
             if (rc || a.K % (2 * F) == 0) return rc;
-            return go(boo_stream_kernel<T, F, VEC, D, DF, 4, false, A32>, 4, 1, full);
+            return wg4 ? go(boo_stream_kernel<T, F, VEC, D, DF, 4, false, A32>, 4, 1, full)
+                       : go(boo_stream_kernel<T, F, VEC, D, DF, 1, false, A32>, 1, 1, full);
         }
     }
     if (full > 0) {
@@ -1692,14 +1801,12 @@ int launch_long_rows(const int* long_rows, int n_long, const I* indptr, const I*
     if (vec) {
         constexpr int V = 16 / sizeof(T);
         const dim3 grid(n_long, (K + 16 * V - 1) / (16 * V), batch);
-        hipLaunchKernelGGL((rows_long_kernel<T, I, V>), grid, dim3(256), 0, s, long_rows, indptr,
-                           col_ind, vals, X, Y, rows, cols, K);
-    } else {
-        const dim3 grid(n_long, (K + 15) / 16, batch);
-        hipLaunchKernelGGL((rows_long_kernel<T, I, 1>), grid, dim3(256), 0, s, long_rows, indptr,
-                           col_ind, vals, X, Y, rows, cols, K);
+        return launch("rows_long_kernel", rows_long_kernel<T, I, V>, grid, dim3(256), s, long_rows, indptr,
+                      col_ind, vals, X, Y, rows, cols, K);
     }
-    return check_launch("rows_long_kernel");
+    const dim3 grid(n_long, (K + 15) / 16, batch);
+    return launch("rows_long_kernel", rows_long_kernel<T, I, 1>, grid, dim3(256), s, long_rows, indptr, col_ind,
+                  vals, X, Y, rows, cols, K);
 }
 
 // Workspace: the partial slots of split slices, then (256-byte aligned) the
@@ -1715,9 +1822,8 @@ int launch_boo_rows_l(const spmm_boo_desc* A, const T* X, T* Y, int K, int batch
     const int n_short = A->n_crow - A->n_crow_long;
     if (n_short <= 0) return SPMM_OK;
     const dim3 grid(round_up8((n_short + RPB - 1) / RPB), (K + LPR * VEC - 1) / (LPR * VEC), batch);
-    hipLaunchKernelGGL((boo_rows_kernel<T, VEC, LPR>), grid, dim3(256), 0, s, A->crow_ptr, A->crow_id,
-                       A->ccol, static_cast<const T*>(A->cval), n_short, X, Y, A->rows, A->cols, K);
-    return check_launch("boo_rows_kernel");
+    return launch("boo_rows_kernel", boo_rows_kernel<T, VEC, LPR>, grid, dim3(256), s, A->crow_ptr, A->crow_id,
+                  A->ccol, static_cast<const T*>(A->cval), n_short, X, Y, A->rows, A->cols, K);
 }
 
 template <typename T, int VEC>
@@ -1741,18 +1847,14 @@ int launch_boo_rows(const spmm_boo_desc* A, const T* X, T* Y, int K, int batch, 
     if (A->n_gtask > 0) {
         const int v = vec ? V : 1;
         const dim3 grid(A->n_gtask, (K + 16 * v - 1) / (16 * v), batch);
-        if (vec)
-            hipLaunchKernelGGL((gather_chunk_kernel<T, V>), grid, dim3(256), 0, s, A->gtask, A->ccol,
-                               static_cast<const T*>(A->cval), X, P2, A->cols, K, batch);
-        else
-            hipLaunchKernelGGL((gather_chunk_kernel<T, 1>), grid, dim3(256), 0, s, A->gtask, A->ccol,
-                               static_cast<const T*>(A->cval), X, P2, A->cols, K, batch);
-        rc = check_launch("gather_chunk_kernel");
+        rc = vec ? launch("gather_chunk_kernel", gather_chunk_kernel<T, V>, grid, dim3(256), s, A->gtask, A->ccol,
+                          static_cast<const T*>(A->cval), X, P2, A->cols, K, batch)
+                 : launch("gather_chunk_kernel", gather_chunk_kernel<T, 1>, grid, dim3(256), s, A->gtask, A->ccol,
+                          static_cast<const T*>(A->cval), X, P2, A->cols, K, batch);
         if (rc) return rc;
     }
-    hipLaunchKernelGGL((gather_fix_kernel<T>), dim3(A->n_crow_long, 1, batch), dim3(256), 0, s, A->gtask_ptr,
-                       A->crow_id, A->n_crow - A->n_crow_long, (const T*)P2, Y, A->rows, K, batch);
-    return check_launch("gather_fix_kernel");
+    return launch("gather_fix_kernel", gather_fix_kernel<T>, dim3(A->n_crow_long, 1, batch), dim3(256), s,
+                  A->gtask_ptr, A->crow_id, A->n_crow - A->n_crow_long, (const T*)P2, Y, A->rows, K, batch);
 }
 
 template <typename T>
@@ -1786,9 +1888,8 @@ int boo_matmul_t(const spmm_boo_desc* A, const void* Xv, void* Yv, int64_t batch
 
     if (A->cols == 0) {  // no entries: Y = 0
         const size_t n = (size_t)batch * (size_t)A->rows * (size_t)K;
-        hipLaunchKernelGGL((fill_zero_kernel<T>), dim3((unsigned)std::min<size_t>((n + 255) / 256, 65535)),
-                           dim3(256), 0, s, Y, n);
-        return check_launch("fill_zero_kernel");
+        return launch("fill_zero_kernel", fill_zero_kernel<T>,
+                      dim3((unsigned)std::min<size_t>((n + 255) / 256, 65535)), dim3(256), s, Y, n);
     }
     StreamArgs<T> a;
     a.rows = A->rows;
@@ -1825,9 +1926,8 @@ int boo_matmul_t(const spmm_boo_desc* A, const void* Xv, void* Yv, int64_t batch
     }
     if (A->n_splits > 0) {
         const dim3 grid(A->n_splits, 1, (unsigned)batch);
-        hipLaunchKernelGGL((boo_fixup_kernel<T>), grid, dim3(256), 0, s, A->splits, A->row_ids,
-                           (const T*)ws, Y, A->rows, (int)K, (int)batch);
-        rc = check_launch("boo_fixup_kernel");
+        rc = launch("boo_fixup_kernel", boo_fixup_kernel<T>, grid, dim3(256), s, A->splits, A->row_ids,
+                    (const T*)ws, Y, A->rows, (int)K, (int)batch);
         if (rc) return rc;
     }
     return launch_long_rows<T, int>(A->long_rows, A->n_long, A->rem_indptr, A->rem_col_ind,
@@ -1835,15 +1935,38 @@ int boo_matmul_t(const spmm_boo_desc* A, const void* Xv, void* Yv, int64_t batch
                                     (int)K, (int)batch, s);
 }
 
+// Blocks of X in flight per wave (1 measured best on configs 2 and 5, and
+// no different on config 3: the walk, not X latency, sets the pace).
+#ifndef SPMM_PBR_DEPTH_SMALL
+#define SPMM_PBR_DEPTH_SMALL 1   // 256-byte feature tiles (64 float / 32 double)
+#endif
+#ifndef SPMM_PBR_DEPTH_BIG
+#define SPMM_PBR_DEPTH_BIG 1     // 1 KiB feature tiles
+#endif
+
+// X of one batch above this many bytes: small feature tiles, one launch each
+// (spmm_pbr_set_slab_bytes; 0, the default: never).
+std::atomic<long long> g_pbr_slab_bytes{0};
+
+// serial: one launch per feature tile, in order, so the X columns of one tile
+// (cols x KT) stay in the MALL while every stripe reads them; otherwise one
+// launch over all tiles (grid.y), whose stripes read every tile's X at once.
 template <typename T, typename I, int BR, int KT, int VEC>
-int launch_pbr(const PbrArgs<T, I>& a, int batch, hipStream_t s) {
-    const dim3 grid(round_up8(a.n_stripes), (a.K + KT - 1) / KT, batch);
+int launch_pbr(const PbrArgs<T, I>& a, int batch, bool serial, hipStream_t s) {
+    const int nkt = (a.K + KT - 1) / KT;
     // 32-bit X offsets when one batch's X is under 4 GiB
-    if ((uint64_t)a.cols * (uint64_t)a.K * sizeof(T) < (1ull << 32))
-        hipLaunchKernelGGL((pbr_stripe_kernel<T, I, BR, KT, VEC, true>), grid, dim3(64), 0, s, a);
-    else
-        hipLaunchKernelGGL((pbr_stripe_kernel<T, I, BR, KT, VEC, false>), grid, dim3(64), 0, s, a);
-    return check_launch("pbr_stripe_kernel");
+    const bool a32 = (uint64_t)a.cols * (uint64_t)a.K * sizeof(T) < (1ull << 32);
+    // blocks in flight per wave: X registers per block are STAGE_ITERS * VEC
+    constexpr int PD = KT * (int)sizeof(T) <= 256 ? SPMM_PBR_DEPTH_SMALL : SPMM_PBR_DEPTH_BIG;
+    auto kern = a32 ? pbr_stripe_kernel<T, I, BR, KT, VEC, PD, true> : pbr_stripe_kernel<T, I, BR, KT, VEC, PD, false>;
+    if (!serial) return launch("pbr_stripe_kernel", kern, dim3(round_up8(a.n_stripes), nkt, batch), dim3(64), s, a);
+    for (int kt = 0; kt < nkt; ++kt) {
+        PbrArgs<T, I> ak = a;
+        ak.kt0 = kt;
+        const int rc = launch("pbr_stripe_kernel", kern, dim3(round_up8(a.n_stripes), 1, batch), dim3(64), s, ak);
+        if (rc) return rc;
+    }
+    return SPMM_OK;
 }
 
 // KT (tile features) is 64 or 256 (float) / 32 or 128 (double); VEC is the
@@ -1852,19 +1975,22 @@ template <typename T, typename I, int BR>
 int pbr_dispatch_br(const PbrArgs<T, I>& a, int batch, hipStream_t s) {
     constexpr int small_kt = 256 / (int)sizeof(T);
     constexpr int big_kt = 1024 / (int)sizeof(T);
-    const bool big = a.K >= big_kt;
+    // X too big for the MALL: small feature tiles, one launch each
+    const long long slab = g_pbr_slab_bytes.load(std::memory_order_relaxed);
+    const bool serial = slab > 0 && a.K > small_kt && (long long)a.cols * a.K * (long long)sizeof(T) > slab;
+    const bool big = a.K >= big_kt && !serial;
     const int F = (big ? big_kt : small_kt) / (64 / BR);
     const int full = 16 / (int)sizeof(T);
     int vec = 1;
     if (F % full == 0 && a.K % full == 0 && aligned16(a.X) && aligned16(a.Y)) vec = full;
     if (big) {
-        if (vec > 1) return launch_pbr<T, I, BR, big_kt, 16 / sizeof(T)>(a, batch, s);
-        return launch_pbr<T, I, BR, big_kt, 1>(a, batch, s);
+        if (vec > 1) return launch_pbr<T, I, BR, big_kt, 16 / sizeof(T)>(a, batch, false, s);
+        return launch_pbr<T, I, BR, big_kt, 1>(a, batch, false, s);
     }
     if constexpr ((small_kt / (64 / BR)) % (16 / sizeof(T)) == 0) {
-        if (vec > 1) return launch_pbr<T, I, BR, small_kt, 16 / sizeof(T)>(a, batch, s);
+        if (vec > 1) return launch_pbr<T, I, BR, small_kt, 16 / sizeof(T)>(a, batch, serial, s);
     }
-    return launch_pbr<T, I, BR, small_kt, 1>(a, batch, s);
+    return launch_pbr<T, I, BR, small_kt, 1>(a, batch, serial, s);
 }
 
 template <typename T, typename I>
@@ -1884,6 +2010,7 @@ int pbr_matmul_t(const spmm_pbr_desc* A, const void* Xv, void* Yv, int64_t batch
     a.K = (int)K;
     a.n_stripes = (int)n_stripes;
     a.long_threshold = A->long_threshold;
+    a.kt0 = 0;
     a.codes = A->codes;
     a.coords = static_cast<const I*>(A->coords);
     a.offsets = static_cast<const I*>(A->offsets);
@@ -2116,6 +2243,14 @@ int spmm_boo_matmul_noalloc(const spmm_boo_desc* A, spmm_dtype dtype, const void
     return spmm_boo_matmul(A, dtype, X, Y, batch, K, ws, need > 0 ? NOALLOC_SCRATCH_BYTES : 0, stream);
 }
 
+int spmm_pbr_set_slab_bytes(int64_t bytes) {
+    if (bytes < 0) return fail(SPMM_EINVAL, "negative PBR slab size");
+    g_pbr_slab_bytes.store(bytes, std::memory_order_relaxed);
+    return SPMM_OK;
+}
+
+int64_t spmm_pbr_get_slab_bytes(void) { return g_pbr_slab_bytes.load(std::memory_order_relaxed); }
+
 int spmm_pbr_matmul(const spmm_pbr_desc* A, spmm_dtype dtype, const void* X, void* Y,
                     int64_t batch, int64_t K, void* stream) {
     if (!A) return fail(SPMM_EINVAL, "null PBR descriptor");
@@ -2131,6 +2266,78 @@ int spmm_pbr_matmul(const spmm_pbr_desc* A, spmm_dtype dtype, const void* X, voi
         return i64 ? pbr_matmul_t<double, int64_t>(A, X, Y, batch, K, s)
                    : pbr_matmul_t<double, int32_t>(A, X, Y, batch, K, s);
     return fail(SPMM_EINVAL, "unknown dtype %d", (int)dtype);
+}
+
+// ---------------------------------------------------------------------------
+// Launch introspection: the multiply's own dispatch, recorded instead of
+// launched, then each kernel's attributes and occupancy from the runtime.
+// ---------------------------------------------------------------------------
+
+namespace {
+
+struct RecordGuard {
+    explicit RecordGuard(std::vector<LaunchRec>* r) { t_record = r; }
+    ~RecordGuard() { t_record = nullptr; }
+};
+
+int describe_launches(const std::vector<LaunchRec>& recs, spmm_launch_info* out, int32_t cap, int32_t* n_out) {
+    if (n_out) *n_out = (int32_t)recs.size();
+    for (size_t i = 0; i < recs.size() && (int64_t)i < cap; ++i) {
+        const LaunchRec& r = recs[i];
+        spmm_launch_info& o = out[i];
+        std::memset(&o, 0, sizeof o);
+        o.kernel = r.name;
+        o.grid[0] = r.grid.x;
+        o.grid[1] = r.grid.y;
+        o.grid[2] = r.grid.z;
+        o.block = r.block.x * r.block.y * r.block.z;
+        hipFuncAttributes fa;
+        hipError_t e = hipFuncGetAttributes(&fa, r.fn);
+        if (e != hipSuccess) return fail(SPMM_ELAUNCH, "hipFuncGetAttributes(%s): %s", r.name, hipGetErrorString(e));
+        o.registers = fa.numRegs;
+        o.scratch_bytes = (int32_t)fa.localSizeBytes;
+        o.lds_bytes = (int32_t)fa.sharedSizeBytes;
+        o.max_threads = fa.maxThreadsPerBlock;
+        int nb = 0;
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, r.fn, (int)o.block, 0);
+        if (e != hipSuccess)
+            return fail(SPMM_ELAUNCH, "hipOccupancyMaxActiveBlocksPerMultiprocessor(%s): %s", r.name,
+                        hipGetErrorString(e));
+        o.wgs_per_cu = nb;
+    }
+    return SPMM_OK;
+}
+
+// Stand-in operand addresses for a recorded dispatch: nothing is launched, so
+// they are never dereferenced; only their alignment steers the dispatch.
+const void* stand_in(const void* p) { return p ? p : reinterpret_cast<const void*>(uintptr_t(1) << 12); }
+
+}  // namespace
+
+int spmm_boo_launch_info(const spmm_boo_desc* A, spmm_dtype dtype, const void* X, const void* Y, int64_t batch,
+                         int64_t K, spmm_launch_info* out, int32_t cap, int32_t* n_out) {
+    if (cap < 0 || (cap > 0 && !out)) return fail(SPMM_EINVAL, "null launch info array");
+    std::vector<LaunchRec> recs;
+    int rc;
+    {
+        RecordGuard g(&recs);
+        void* ws = const_cast<void*>(stand_in(nullptr));
+        rc = spmm_boo_matmul(A, dtype, stand_in(X), const_cast<void*>(stand_in(Y)), batch, K, ws, SIZE_MAX,
+                             nullptr);
+    }
+    return rc ? rc : describe_launches(recs, out, cap, n_out);
+}
+
+int spmm_pbr_launch_info(const spmm_pbr_desc* A, spmm_dtype dtype, const void* X, const void* Y, int64_t batch,
+                         int64_t K, spmm_launch_info* out, int32_t cap, int32_t* n_out) {
+    if (cap < 0 || (cap > 0 && !out)) return fail(SPMM_EINVAL, "null launch info array");
+    std::vector<LaunchRec> recs;
+    int rc;
+    {
+        RecordGuard g(&recs);
+        rc = spmm_pbr_matmul(A, dtype, stand_in(X), const_cast<void*>(stand_in(Y)), batch, K, nullptr);
+    }
+    return rc ? rc : describe_launches(recs, out, cap, n_out);
 }
 
 int spmm_csr_naive(const void* indptr, const void* col_ind, const void* vals, spmm_itype itype,

@@ -267,6 +267,33 @@ def pbr_batched_matmul_cuda(pbr_mat, x: torch.Tensor, csr_mode: int = 0,
     return y
 
 
+def set_pbr_slab_bytes(nbytes: int) -> None:
+    """Process-wide launch knob (like the reference's set_boo_feat_block):
+    when one batch's X is larger than ``nbytes`` (0, the default: never), the
+    stripe kernel runs its feature tiles one launch after another at 64
+    features (32 for float64), so one tile's X can stay in the last-level
+    cache.  Results are the same either way."""
+    core.pbr_set_slab_bytes(int(nbytes))
+
+
+def get_pbr_slab_bytes() -> int:
+    return int(core.pbr_get_slab_bytes())
+
+
+def pbr_launch_info(pbr_mat, features: int, batch: int = 1, x=None) -> list:
+    """The kernels ``pbr_matmul(pbr_mat, X)`` launches for ``batch`` x
+    ``features`` columns, in launch order, with the runtime's attributes of
+    each kernel instance (the same keys as ``boo_launch_info``): the
+    multiply's own dispatch, recorded instead of enqueued.  ``x`` (optional)
+    supplies the alignment that steers the dispatch."""
+    meta = pbr_mat._gpu_meta
+    if meta is None:
+        raise RuntimeError("PBRMatrix is not on GPU. Call .to('cuda') first.")
+    with torch.cuda.device(meta.codes.device):
+        xp = int(x.data_ptr()) if x is not None else 0
+        return core.pbr_launch_info(meta.desc, _DTYPE_CODE[meta.data.dtype], xp, 0, int(batch), int(features))
+
+
 def pbr_batched_matmul_chunkcols_cuda(pbr_mat, x, csr_mode: int = 0, smem_size: int = 2048):
     """The reference's experimental chunkcols variant: same result, served by
     the stripe kernel."""

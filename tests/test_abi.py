@@ -50,6 +50,12 @@ def test_version_and_error_path_without_gpu(lib):
     assert rc == 1 and b'null' in lib.spmm_last_error()
     rc = lib.spmm_pbr_matmul(None, 0, None, None, ctypes.c_int64(1), ctypes.c_int64(8), None)
     assert rc == 1
+    n = ctypes.c_int32(-1)
+    for fn in (lib.spmm_boo_launch_info, lib.spmm_pbr_launch_info):
+        rc = fn(None, 0, None, None, ctypes.c_int64(1), ctypes.c_int64(8), None, 0, ctypes.byref(n))
+        assert rc == 1 and b'null' in lib.spmm_last_error()
+        rc = fn(None, 0, None, None, ctypes.c_int64(1), ctypes.c_int64(8), None, 4, ctypes.byref(n))
+        assert rc == 1 and b'launch info' in lib.spmm_last_error()
 
 
 def test_stage_create_rejects_bad_arguments_without_gpu(lib):
@@ -60,3 +66,12 @@ def test_stage_create_rejects_bad_arguments_without_gpu(lib):
     rc = lib.spmm_boo_stage_sizes(None, None)
     assert rc == 1
     lib.spmm_boo_stage_destroy(None)              # a null handle is accepted
+
+
+def test_pbr_slab_knob_without_gpu(lib):
+    lib.spmm_last_error.restype = ctypes.c_char_p
+    lib.spmm_pbr_get_slab_bytes.restype = ctypes.c_int64
+    assert lib.spmm_pbr_set_slab_bytes(ctypes.c_int64(-1)) == 1 and b'negative' in lib.spmm_last_error()
+    assert lib.spmm_pbr_set_slab_bytes(ctypes.c_int64(123 << 20)) == 0
+    assert lib.spmm_pbr_get_slab_bytes() == 123 << 20
+    assert lib.spmm_pbr_set_slab_bytes(ctypes.c_int64(0)) == 0 and lib.spmm_pbr_get_slab_bytes() == 0
