@@ -68,10 +68,15 @@ def time_steps(fns, steps, warmup, torch):
     return wall / steps * 1e3, e0.elapsed_time(e1) / steps
 
 
-def cpu_baseline(A, spec, cfg, fmt):
-    """The reference's own CPU op for the measured format
-    (boo_batched_matmul_cpu or pbr_batched_matmul_cpu, single thread), compiled
-    from its sources into oracle/_ref, on the same config."""
+def cpu_baseline(A, spec, cfg, fmt, y_gpu):
+    """The reference's own CPU ops, compiled from its sources into
+    oracle/_ref, on the same matrix and X (seed 0), single-threaded:
+    boo_batched_matmul_cpu (boo_matrix.cpp:336-396), pbr_batched_matmul_cpu
+    (pbr_matrix.cpp:17-68) and the CSR row loop (boo_matrix.cpp:374-383, run
+    over the whole matrix by building the BOO with every entry in the
+    remainder).  `value` is the measured format's op; the GPU's Y for the
+    same X (y_gpu: {'boo': .., 'pbr': ..}) is compared with the reference
+    op's Y under the north star's bar, max |Y_gpu - Y_ref| / (|A||X|)."""
     import importlib
     import torch
     ref_dir = ROOT / 'oracle' / '_ref'
@@ -81,29 +86,51 @@ def cpu_baseline(A, spec, cfg, fmt):
     ref = importlib.import_module('torch_fast_spdmm_core')
     sys.path.insert(0, str(ROOT))
     from oracle import oracle as O
-    K = spec['K']
-    if fmt == 'boo':
-        rl = O.identity_labels(A.shape[0], 32)
-        b = ref.csr_to_boo(A.indptr, A.indices, A.data, A.shape[0], A.shape[1], rl, rl, 2, 4, 0)
-        op = ref.boo_batched_matmul_cpu
-    else:
-        b = ref.csr_to_pbr(A.indptr, A.indices, A.data, A.shape[0], A.shape[1], 8, 8,
-                           spec.get('pbr_threshold', 4))
-        op = ref.pbr_batched_matmul_cpu
     from spmm_amd import matrices as M
+    K = spec['K']
     x = torch.from_numpy(M.dense_x(A.shape[1], K))
+    rl = O.identity_labels(A.shape[0], 32)
+    cl = O.identity_labels(A.shape[1], 32)
+    thr = spec.get('pbr_threshold', 4)
+    builds = {
+        'boo': lambda: ref.csr_to_boo(A.indptr, A.indices, A.data, A.shape[0], A.shape[1], rl, cl, 2, 4, 0),
+        'pbr': lambda: ref.csr_to_pbr(A.indptr, A.indices, A.data, A.shape[0], A.shape[1], 8, 8, thr),
+        # threshold above any block's count: every entry goes to the remainder CSR
+        'csr': lambda: ref.csr_to_boo(A.indptr, A.indices, A.data, A.shape[0], A.shape[1], rl, cl, 2,
+                                      1 << 30, 0),
+    }
+    ops = {'boo': ref.boo_batched_matmul_cpu, 'pbr': ref.pbr_batched_matmul_cpu, 'csr': ref.boo_batched_matmul_cpu}
+    names = {'boo': 'boo_batched_matmul_cpu', 'pbr': 'pbr_batched_matmul_cpu',
+             'csr': 'CSR row loop (boo_batched_matmul_cpu, all entries in the remainder)'}
+    _, bound = O.spmm_reference(A, x.numpy())
     nthreads = torch.get_num_threads()
     torch.set_num_threads(1)
+    res = {}
+    # all three ops on configs up to ~8M nonzeros (about 10 s of CPU work);
+    # above that only the measured format's op keeps the run bounded
+    which = ('boo', 'pbr', 'csr') if A.nnz <= 8_000_000 else (fmt,)
     try:
-        op(b, x)                                            # warmup
-        ts = []
-        for _ in range(3):
-            t0 = time.perf_counter()
-            op(b, x)
-            ts.append(time.perf_counter() - t0)
+        for k in which:
+            b = builds[k]()
+            y = ops[k](b, x)                                    # warmup, and the reference's Y
+            ts = []
+            for _ in range(3):
+                t0 = time.perf_counter()
+                ops[k](b, x)
+                ts.append(time.perf_counter() - t0)
+            t = sorted(ts)[1]
+            r = {'gflops': round(2.0 * A.nnz * K / t / 1e9, 3), 'ms_per_call': round(t * 1e3, 1), 'op': names[k]}
+            yg = y_gpu.get(k)
+            if yg is not None:
+                err = np.abs(np.asarray(yg, np.float64) - y.numpy()[0].astype(np.float64))
+                with np.errstate(divide='ignore', invalid='ignore'):
+                    ratio = np.where(bound > 0, err / np.where(bound > 0, bound, 1), np.where(err > 0, np.inf, 0))
+                r['gpu_vs_reference_max_ratio'] = float(f'{float(ratio.max()):.3e}')
+                r['gpu_vs_reference_ok'] = bool(np.all(err <= 1e-5 * bound))
+            res[k] = r
+            del b
     finally:
         torch.set_num_threads(nthreads)
-    t = sorted(ts)[1]
     cpu_model = platform.processor() or 'x86_64'
     try:
         with open('/proc/cpuinfo') as f:
@@ -113,11 +140,11 @@ def cpu_baseline(A, spec, cfg, fmt):
                     break
     except OSError:
         pass
-    return {'value': round(2.0 * A.nnz * K / t / 1e9, 3), 'unit': 'GFLOP/s', 'cores': 1,
-            'kind': 'reference',
-            'sample': f'full config-{cfg} matrix, K={K}: {fmt}_batched_matmul_cpu, 1 warmup + median of 3 '
-                      f'({t * 1e3:.0f} ms/call), single thread',
-            'host_cpu': cpu_model, 'host_cores_available': len(os.sched_getaffinity(0))}
+    main = res[fmt]
+    return {'value': main['gflops'], 'unit': 'GFLOP/s', 'cores': 1, 'kind': 'reference',
+            'sample': f'full config-{cfg} matrix, K={K}, X seed 0: {names[fmt]}, 1 warmup + median of 3 '
+                      f'({main["ms_per_call"]:.0f} ms/call), single thread',
+            'ops': res, 'host_cpu': cpu_model, 'host_cores_available': len(os.sched_getaffinity(0))}
 
 
 def vendor_baseline(S, A, K, Xs, steps, warmup, O, torch):
@@ -257,6 +284,8 @@ def main():
     ap.add_argument('--no-vendor', action='store_true', help='skip the rocSPARSE baseline')
     ap.add_argument('--no-cpp-timed', action='store_true',
                     help='skip the natively timed single-call BOO figure (keeps a kernel trace to the timed steps)')
+    ap.add_argument('--pbr-slab-mb', type=float, default=0.0,
+                    help='PBR launch knob: X above this many MiB runs its feature tiles one launch each (0: never)')
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
@@ -268,6 +297,7 @@ def main():
     sys.path.insert(0, str(ROOT))
     import spmm_amd as S
     from spmm_amd import matrices as M
+    S.set_pbr_slab_bytes(int(args.pbr_slab_mb * (1 << 20)))
 
     if args.calibrate_copy:
         calibrate_copy(torch)
@@ -295,8 +325,10 @@ def main():
     ms_wall = ms_ev_mean = ms_api = ratio = None
 
     # ---- BOO (headline when the config has it)
+    y_gpu = {}
     if has_boo:
         ms_wall, ms_ev_mean, ms_api, ratio = bench_boo(S, A, K, Xs, Ys, dev, stream, args, O, torch)
+        y_gpu['boo'] = Ys[0][0].cpu().numpy()
 
     # ---- PBR on the same matrix
     pbr = {}
@@ -309,7 +341,8 @@ def main():
                                    int(Ys[i].data_ptr()), 1, K, int(stream))
         pbr_step(0)
         torch.cuda.synchronize()
-        pratio, pok = O.within_bound(Ys[0][0].cpu().numpy(), A, Xs[0].cpu().numpy(), 1e-5)
+        y_gpu['pbr'] = Ys[0][0].cpu().numpy()
+        pratio, pok = O.within_bound(y_gpu['pbr'], A, Xs[0].cpu().numpy(), 1e-5)
         if not pok:
             _log(f'PBR PARITY FAILURE: {pratio:.3e}')
             sys.exit(1)
@@ -332,7 +365,7 @@ def main():
     else:
         workload = f'cfg{args.config}_{spec["name"]}_pbr8x8_thr{spec.get("pbr_threshold", 4)}_K{K}'
         fmt_desc = f'PBR 8x8, min_nnz_per_block {spec.get("pbr_threshold", 4)}'
-    cpu = None if args.no_cpu_baseline else cpu_baseline(A, spec, args.config, fmt)
+    cpu = None if args.no_cpu_baseline else cpu_baseline(A, spec, args.config, fmt, y_gpu)
     vendor = None if args.no_vendor else vendor_baseline(S, A, K, Xs, min(args.steps, 20), 3, O, torch)
     cpp_timed = (cpp_timed_boo(S, A, K, Xs[0], min(args.steps, 20), torch)
                  if has_boo and not args.no_cpp_timed else None)
