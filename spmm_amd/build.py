@@ -44,12 +44,12 @@ ARCH = os.environ.get('SPMM_AMD_ARCH', 'gfx950')
 HIPCC_FLAGS = [
     '-O3', '-std=c++17', f'--offload-arch={ARCH}', '-fPIC', '-shared',
     '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
-    '-Wall', '-Wno-unused-function',
+    '-Wall', '-Wno-unused-function', '-pthread',
 ]
 
 # -ffp-contract=off keeps the CPU ops' y += a*x as a separate multiply and add,
 # the rounding of the reference's CPU loops.
-CXX_FLAGS = ['-O3', '-std=c++17', '-fPIC', '-shared', '-ffp-contract=off', '-fvisibility=hidden']
+CXX_FLAGS = ['-O3', '-std=c++17', '-fPIC', '-shared', '-ffp-contract=off', '-fvisibility=hidden', '-pthread']
 
 
 def _run(cmd):

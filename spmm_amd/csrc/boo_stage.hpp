@@ -40,6 +40,7 @@
 #include <cstring>
 #include <stdexcept>
 #include <string>
+#include <thread>
 #include <type_traits>
 #include <vector>
 
@@ -84,6 +85,8 @@ constexpr int GATHER_SKEWED_LONG = 32;
 // order already keeps hub columns hot), hence a gain of 2 to switch.
 constexpr int GATHER_REUSE_WINDOW = 8192;
 constexpr double GATHER_REORDER_GAIN = 2.0;
+// Both orders are compared on their first GATHER_REUSE_SAMPLE entries.
+constexpr long long GATHER_REUSE_SAMPLE = 1ll << 23;
 
 // Record stream (float, groups of 4): each wave's tiles again, one
 // contiguous, 16-byte aligned record per step, so that a wave moves a whole
@@ -145,6 +148,26 @@ struct Staged {
     size_t n_tiles() const { return tiles.size() / TILE_WORDS; }
 };
 
+// f(begin, end) over [0, n) in contiguous ranges on up to 16 threads (the
+// calling thread takes the first); small n runs inline.  f must not throw.
+template <typename F>
+inline void par_ranges(size_t n, F&& f) {
+    const unsigned hw = std::thread::hardware_concurrency();
+    const size_t nt = std::min<size_t>(std::min<size_t>(hw ? hw : 1, 16), (n + 4095) / 4096);
+    if (nt <= 1) {
+        f((size_t)0, n);
+        return;
+    }
+    const size_t per = (n + nt - 1) / nt;
+    std::vector<std::thread> th;
+    for (size_t t = 1; t < nt; ++t) {
+        const size_t b = t * per, e = std::min(n, b + per);
+        if (b < e) th.emplace_back([&f, b, e]() { f(b, e); });
+    }
+    f((size_t)0, std::min(n, per));
+    for (std::thread& x : th) x.join();
+}
+
 // One nonzero on its way into a tile.
 struct Ent {
     int32_t src;      // index of the value in its source array
@@ -181,7 +204,6 @@ public:
         S.group = G_;
         S.tcols.assign(in_.col_ids, in_.col_ids + in_.cols);
         collect_slices(S);
-        classify_slices();
         for (const Slice& sl : slices_) {  // long remainder rows of the tile stream's slices
             if (sl.csr) continue;
             S.n_stream_rows += sl.nr;
@@ -207,7 +229,8 @@ private:
         size_t r0, r1;  // remainder entries in pool_ (lc = 0; column in rcol_)
         size_t g0, g1;  // its long remainder rows in longs_
         long long nnz;
-        bool csr;       // rows go to the gather pass, not the tile stream
+        bool csr;       // rows go to the gather pass, not the tile stream; its short
+                        // remainder is then read from the input CSR, not pool_
     };
     struct LongRow {
         int32_t lr, row;
@@ -258,6 +281,19 @@ private:
 
     void collect_slices(Staged& S) {
         check_indices();
+        {
+            const size_t n_ent = (size_t)(in_.num_blocks > 0 ? in_.blk_nz_ptr[in_.num_blocks] : 0) +
+                                 (size_t)in_.rem_indptr[in_.rows];
+            pool_.reserve(n_ent);
+            rcol_.reserve(n_ent);
+        }
+        // Send empty slices, and slices whose tiles would stage more X rows
+        // than min_reuse per entry allows, to the gather pass.  A slice's
+        // tiles stage every column of each block chunk it touches plus its
+        // remainder's distinct columns (counted with stamp: the last slice
+        // that counted the column).
+        const bool use_stamp = min_reuse_ > 0.0f;
+        std::vector<int32_t> stamp(use_stamp ? (size_t)in_.cols : 0, -1);
         int blk = 0;
         std::vector<Ent> ents;
         for (int rg = 0; rg < in_.n_row_groups; ++rg) {
@@ -318,6 +354,11 @@ private:
                 sl.c1 = chunks_.size();
                 sl.r0 = pool_.size();
                 sl.g0 = longs_.size();
+                // the slice's short remainder: its entries and distinct
+                // columns decide tile stream or gather pass (classify)
+                long long staged = 0;
+                for (size_t c = sl.c0; c < sl.c1; ++c) staged += chunks_[c].nc;
+                const int32_t si = (int32_t)slices_.size();
                 for (int lr = 0; lr < sl.nr; ++lr) {
                     const int row = in_.row_ids[sl.row_off + lr];
                     if (row < 0 || row >= in_.rows) throw std::invalid_argument("row_ids out of range");
@@ -327,15 +368,31 @@ private:
                         longs_.push_back(LongRow{lr, row});
                         continue;
                     }
-                    for (int j = rs; j < re; ++j) {
-                        pool_.push_back(Ent{j, (uint8_t)lr, 0, 1, 0});
-                        rcol_.resize(pool_.size());
-                        rcol_.back() = in_.rem_col_ind[j];
-                    }
                     sl.nnz += re - rs;
+                    if (use_stamp)
+                        for (int j = rs; j < re; ++j) {
+                            const int32_t col = in_.rem_col_ind[j];
+                            if (stamp[col] != si) {
+                                stamp[col] = si;
+                                ++staged;
+                            }
+                        }
+                }
+                sl.g1 = longs_.size();
+                sl.csr = use_stamp && (sl.nnz == 0 || (double)sl.nnz < (double)min_reuse_ * (double)staged);
+                if (!sl.csr) {
+                    rcol_.resize(pool_.size());  // block entries have no entry here
+                    for (int lr = 0; lr < sl.nr; ++lr) {
+                        const int row = in_.row_ids[sl.row_off + lr];
+                        const int rs = in_.rem_indptr[row], re = in_.rem_indptr[row + 1];
+                        if (re == rs || re - rs > long_threshold_) continue;
+                        for (int j = rs; j < re; ++j) {
+                            pool_.push_back(Ent{j, (uint8_t)lr, 0, 1, 0});
+                            rcol_.push_back(in_.rem_col_ind[j]);
+                        }
+                    }
                 }
                 sl.r1 = pool_.size();
-                sl.g1 = longs_.size();
                 slices_.push_back(sl);
             }
         }
@@ -343,30 +400,21 @@ private:
         rcol_.resize(pool_.size());
     }
 
+    // f(lr, j) for each short remainder entry j of gather slice sl, row by
+    // row, from the input CSR (the order pool_ would hold them in).
+    template <typename F>
+    void for_short_rem(const Slice& sl, F&& f) const {
+        for (int lr = 0; lr < sl.nr; ++lr) {
+            const int row = in_.row_ids[sl.row_off + lr];
+            const int rs = in_.rem_indptr[row], re = in_.rem_indptr[row + 1];
+            if (re - rs > long_threshold_) continue;
+            for (int j = rs; j < re; ++j) f(lr, j);
+        }
+    }
+
     // Global column of a pool_ entry of slice chunk c (block) or remainder.
     int32_t ent_col_of(size_t e, const Chunk* c) const {
         return c ? in_.col_ids[c->cid_off + pool_[e].lc] : rcol_[e];
-    }
-
-    // Send empty slices, and slices whose tiles would stage more X rows than
-    // min_reuse per entry allows, to the gather pass.  A slice's tiles stage
-    // every column of each block chunk it touches plus its remainder's
-    // distinct columns.
-    void classify_slices() {
-        if (!(min_reuse_ > 0.0f)) return;
-        std::vector<int32_t> cols;
-        for (Slice& sl : slices_) {
-            if (sl.nnz == 0) {
-                sl.csr = true;
-                continue;
-            }
-            long long staged = 0;
-            for (size_t c = sl.c0; c < sl.c1; ++c) staged += chunks_[c].nc;
-            cols.assign(rcol_.begin() + sl.r0, rcol_.begin() + sl.r1);
-            std::sort(cols.begin(), cols.end());
-            staged += std::unique(cols.begin(), cols.end()) - cols.begin();
-            sl.csr = (double)sl.nnz < (double)min_reuse_ * (double)staged;
-        }
     }
 
     // Entries of each gather row (block entries plus remainder, long or not),
@@ -381,9 +429,10 @@ private:
             cnt.assign((size_t)sl.nr, 0);
             for (size_t c = sl.c0; c < sl.c1; ++c)
                 for (size_t e = chunks_[c].e0; e < chunks_[c].e1; ++e) ++cnt[pool_[e].lr];
-            for (size_t e = sl.r0; e < sl.r1; ++e) ++cnt[pool_[e].lr];
-            for (size_t i = sl.g0; i < sl.g1; ++i)
-                cnt[longs_[i].lr] += in_.rem_indptr[longs_[i].row + 1] - in_.rem_indptr[longs_[i].row];
+            for (int lr = 0; lr < sl.nr; ++lr) {  // short and long remainder rows alike
+                const int row = in_.row_ids[sl.row_off + lr];
+                cnt[lr] += in_.rem_indptr[row + 1] - in_.rem_indptr[row];
+            }
             for (long long c : cnt) {
                 s1 += (double)c;
                 s2 += (double)c * (double)c;
@@ -401,57 +450,97 @@ private:
     // the longer ones follow, each cut into chunk tasks.
     void emit_csr(Staged& S) {
         const int thr = gather_long_threshold();
-        struct RE {
-            int32_t lr, col;
-            int32_t src;
-            int32_t from_rem;
-        };
-        std::vector<RE> v;
-        std::vector<int32_t> long_id, long_ptr(1, 0), long_col;
-        std::vector<T> long_val;
-        S.crow_ptr.assign(1, 0);
-        auto put = [](std::vector<int32_t>& cols, std::vector<char>& vals, int32_t col, T x) {
-            cols.push_back(col);
-            const char* p = reinterpret_cast<const char*>(&x);
-            vals.insert(vals.end(), p, p + sizeof(T));
-        };
-        for (const Slice& sl : slices_) {
-            if (!sl.csr) continue;
-            v.clear();
-            for (size_t c = sl.c0; c < sl.c1; ++c)
-                for (size_t e = chunks_[c].e0; e < chunks_[c].e1; ++e)
-                    v.push_back(RE{pool_[e].lr, ent_col_of(e, &chunks_[c]), pool_[e].src, 0});
-            for (size_t e = sl.r0; e < sl.r1; ++e) v.push_back(RE{pool_[e].lr, rcol_[e], pool_[e].src, 1});
-            for (size_t i = sl.g0; i < sl.g1; ++i) {
-                const int row = longs_[i].row;
-                for (int j = in_.rem_indptr[row]; j < in_.rem_indptr[row + 1]; ++j)
-                    v.push_back(RE{longs_[i].lr, in_.rem_col_ind[j], j, 1});
-            }
-            std::stable_sort(v.begin(), v.end(), [](const RE& a, const RE& b) { return a.lr < b.lr; });
-            size_t k = 0;
-            for (int lr = 0; lr < sl.nr; ++lr) {
-                size_t k1 = k;
-                while (k1 < v.size() && v[k1].lr == lr) ++k1;
-                const int32_t row = in_.row_ids[sl.row_off + lr];
-                const bool is_long = (long long)(k1 - k) > (long long)thr;
-                for (; k < k1; ++k) {
-                    const T x = v[k].from_rem ? in_.rem_vals[v[k].src] : in_.nz_val[v[k].src];
-                    if (is_long) {
-                        long_col.push_back(v[k].col);
-                        long_val.push_back(x);
+        // Pass 1, per gather slice: its rows' entry counts (block entries,
+        // short remainder, long remainder) and its totals of short and long
+        // rows and entries.  Pass 2 fills every slice's share of the output
+        // at offsets from the prefix sums, each row's entries in the order
+        // block entries, short remainder, long remainder.
+        std::vector<size_t> gs;  // gather slices
+        for (size_t i = 0; i < slices_.size(); ++i)
+            if (slices_[i].csr) gs.push_back(i);
+        const size_t ng = gs.size();
+        std::vector<int32_t> rcnt(ng * TILE_ROWS, 0);
+        std::vector<int64_t> n_sr(ng + 1, 0), n_se(ng + 1, 0), n_lr(ng + 1, 0), n_le(ng + 1, 0);
+        par_ranges(ng, [&](size_t b0, size_t b1) {
+            for (size_t k = b0; k < b1; ++k) {
+                const Slice& sl = slices_[gs[k]];
+                int32_t* cnt = &rcnt[k * TILE_ROWS];
+                for (size_t c = sl.c0; c < sl.c1; ++c)
+                    for (size_t e = chunks_[c].e0; e < chunks_[c].e1; ++e) ++cnt[pool_[e].lr];
+                for (int lr = 0; lr < sl.nr; ++lr) {  // short and long remainder rows alike
+                    const int row = in_.row_ids[sl.row_off + lr];
+                    cnt[lr] += in_.rem_indptr[row + 1] - in_.rem_indptr[row];
+                }
+                for (int lr = 0; lr < sl.nr; ++lr) {
+                    if (cnt[lr] > thr) {
+                        ++n_lr[k + 1];
+                        n_le[k + 1] += cnt[lr];
                     } else {
-                        put(S.ccol, S.cval, v[k].col, x);
+                        ++n_sr[k + 1];
+                        n_se[k + 1] += cnt[lr];
                     }
                 }
-                if (is_long) {
-                    long_id.push_back(row);
-                    long_ptr.push_back((int32_t)long_col.size());
-                } else {
-                    S.crow_id.push_back(row);
-                    S.crow_ptr.push_back((int32_t)S.ccol.size());
+            }
+        });
+        for (size_t k = 0; k < ng; ++k) {
+            n_sr[k + 1] += n_sr[k];
+            n_se[k + 1] += n_se[k];
+            n_lr[k + 1] += n_lr[k];
+            n_le[k + 1] += n_le[k];
+        }
+        if (n_se[ng] + n_le[ng] > (int64_t)INT32_MAX) throw std::invalid_argument("too many gather-pass entries");
+        S.crow_id.assign((size_t)n_sr[ng], 0);
+        S.crow_ptr.assign((size_t)n_sr[ng] + 1, 0);
+        S.ccol.assign((size_t)n_se[ng], 0);
+        std::vector<T> short_val((size_t)n_se[ng]);
+        std::vector<int32_t> long_id((size_t)n_lr[ng]), long_ptr((size_t)n_lr[ng] + 1, 0),
+            long_col((size_t)n_le[ng]);
+        std::vector<T> long_val((size_t)n_le[ng]);
+        par_ranges(ng, [&](size_t b0, size_t b1) {
+            std::vector<int32_t> at(TILE_ROWS);
+            for (size_t k = b0; k < b1; ++k) {
+                const Slice& sl = slices_[gs[k]];
+                const int32_t* cnt = &rcnt[k * TILE_ROWS];
+                // each row's first output position (short or long arrays)
+                int64_t sr = n_sr[k], se = n_se[k], lrw = n_lr[k], le = n_le[k];
+                for (int lr = 0; lr < sl.nr; ++lr) {
+                    const int32_t row = in_.row_ids[sl.row_off + lr];
+                    if (cnt[lr] > thr) {
+                        at[lr] = (int32_t)le;
+                        long_id[(size_t)lrw] = row;
+                        le += cnt[lr];
+                        long_ptr[(size_t)++lrw] = (int32_t)le;
+                    } else {
+                        at[lr] = (int32_t)se;
+                        S.crow_id[(size_t)sr] = row;
+                        se += cnt[lr];
+                        S.crow_ptr[(size_t)++sr] = (int32_t)se;
+                    }
+                }
+                auto put = [&](int lr, int32_t col, T x) {
+                    const size_t q = (size_t)at[lr]++;
+                    if (cnt[lr] > thr) {
+                        long_col[q] = col;
+                        long_val[q] = x;
+                    } else {
+                        S.ccol[q] = col;
+                        short_val[q] = x;
+                    }
+                };
+                for (size_t c = sl.c0; c < sl.c1; ++c)
+                    for (size_t e = chunks_[c].e0; e < chunks_[c].e1; ++e)
+                        put(pool_[e].lr, ent_col_of(e, &chunks_[c]), in_.nz_val[pool_[e].src]);
+                for_short_rem(sl, [&](int lr, int j) { put(lr, in_.rem_col_ind[j], in_.rem_vals[j]); });
+                for (size_t i = sl.g0; i < sl.g1; ++i) {
+                    const int row = longs_[i].row;
+                    for (int j = in_.rem_indptr[row]; j < in_.rem_indptr[row + 1]; ++j)
+                        put(longs_[i].lr, in_.rem_col_ind[j], in_.rem_vals[j]);
                 }
             }
-        }
+        });
+        S.cval.resize(short_val.size() * sizeof(T));
+        if (!short_val.empty()) std::memcpy(S.cval.data(), short_val.data(), S.cval.size());
+        std::vector<T>().swap(short_val);
         reorder_short_rows(S);
         S.n_crow_long = (int32_t)long_id.size();
         S.gtask_ptr.assign(1, 0);
@@ -465,24 +554,30 @@ private:
             S.gtask_ptr.push_back((int32_t)(S.gtask.size() / 2));
             S.crow_ptr.push_back(base + long_ptr[i + 1]);
         }
-        for (size_t e = 0; e < long_col.size(); ++e) put(S.ccol, S.cval, long_col[e], long_val[e]);
+        S.ccol.insert(S.ccol.end(), long_col.begin(), long_col.end());
+        const size_t v0 = S.cval.size();
+        S.cval.resize(v0 + long_val.size() * sizeof(T));
+        if (!long_val.empty()) std::memcpy(S.cval.data() + v0, long_val.data(), long_val.size() * sizeof(T));
     }
 
-    // Entries of the short gather rows, taken in `order`, whose column was
-    // named by a row at most GATHER_REUSE_WINDOW positions before (an X row
-    // another row nearby also reads).
-    long long window_reuse(const Staged& S, const std::vector<int32_t>& order) const {
-        std::vector<int32_t> last((size_t)in_.cols, -1);
-        long long hits = 0;
-        for (int32_t p = 0; p < (int32_t)order.size(); ++p) {
+    // Entries among the first GATHER_REUSE_SAMPLE entries of the short gather
+    // rows, taken in `order`, whose column was named by a row at most
+    // GATHER_REUSE_WINDOW positions before (an X row another row nearby also
+    // reads), per entry.  A prefix is enough to tell the two orders apart and
+    // keeps the estimate's cost bounded on large matrices.
+    double window_reuse(const Staged& S, const std::vector<int32_t>& order, std::vector<int32_t>& last) const {
+        std::fill(last.begin(), last.end(), -1);
+        long long hits = 0, seen = 0;
+        for (int32_t p = 0; p < (int32_t)order.size() && seen < GATHER_REUSE_SAMPLE; ++p) {
             const int32_t i = order[p];
             for (int32_t e = S.crow_ptr[i]; e < S.crow_ptr[i + 1]; ++e) {
                 const int32_t c = S.ccol[e];
                 if (last[c] >= 0 && p - last[c] <= GATHER_REUSE_WINDOW) ++hits;
                 last[c] = p;
             }
+            seen += S.crow_ptr[i + 1] - S.crow_ptr[i];
         }
-        return hits;
+        return seen ? (double)hits / (double)seen : 0.0;
     }
 
     // Reorder the short gather rows (S.crow_id/crow_ptr/ccol/cval so far) by
@@ -490,56 +585,69 @@ private:
     // Row i's neighbours are the short rows whose row id is one of its column
     // ids (the matrix read as a graph; any order is correct, this one is
     // local when the matrix is a graph with locality under some labelling).
+    // Breadth first from the unvisited row of least length (ties: slice
+    // order), each row's neighbours in the order of its entries.
     void reorder_short_rows(Staged& S) {
         const int32_t n = (int32_t)S.crow_id.size();
         if (n < 2 || in_.rows != in_.cols) return;
         std::vector<int32_t> pos_of_row((size_t)in_.rows, -1);
         for (int32_t i = 0; i < n; ++i) pos_of_row[S.crow_id[i]] = i;
-        auto deg = [&](int32_t i) { return S.crow_ptr[i + 1] - S.crow_ptr[i]; };
-        // start nodes: unvisited rows by ascending length (ties: slice order)
-        std::vector<int32_t> starts(n);
-        for (int32_t i = 0; i < n; ++i) starts[i] = i;
-        std::stable_sort(starts.begin(), starts.end(), [&](int32_t a, int32_t b) { return deg(a) < deg(b); });
+        // start nodes: rows by ascending length, stable (a counting sort)
+        int32_t max_deg = 0;
+        for (int32_t i = 0; i < n; ++i) max_deg = std::max(max_deg, S.crow_ptr[i + 1] - S.crow_ptr[i]);
+        std::vector<int32_t> first((size_t)max_deg + 2, 0), starts((size_t)n);
+        for (int32_t i = 0; i < n; ++i) ++first[(size_t)(S.crow_ptr[i + 1] - S.crow_ptr[i]) + 1];
+        for (int32_t d = 0; d <= max_deg; ++d) first[(size_t)d + 1] += first[(size_t)d];
+        for (int32_t i = 0; i < n; ++i) starts[(size_t)first[(size_t)(S.crow_ptr[i + 1] - S.crow_ptr[i])]++] = i;
+        // pos_of_row doubles as the visited mark: a row is set to -1 when it
+        // joins the order (one random access per entry, not two)
         std::vector<int32_t> order;
         order.reserve(n);
-        std::vector<char> seen(n, 0);
-        std::vector<int32_t> nb;
         for (int32_t st : starts) {
-            if (seen[st]) continue;
-            seen[st] = 1;
+            int32_t& ps = pos_of_row[S.crow_id[st]];
+            if (ps < 0) continue;
+            ps = -1;
             size_t head = order.size();
             order.push_back(st);
             while (head < order.size()) {
                 const int32_t i = order[head++];
-                nb.clear();
                 for (int32_t e = S.crow_ptr[i]; e < S.crow_ptr[i + 1]; ++e) {
-                    const int32_t j = pos_of_row[S.ccol[e]];
-                    if (j >= 0 && !seen[j]) {
-                        seen[j] = 1;
-                        nb.push_back(j);
+                    int32_t& pj = pos_of_row[S.ccol[e]];
+                    if (pj >= 0) {
+                        order.push_back(pj);
+                        pj = -1;
                     }
                 }
-                std::stable_sort(nb.begin(), nb.end(), [&](int32_t a, int32_t b) { return deg(a) < deg(b); });
-                order.insert(order.end(), nb.begin(), nb.end());
             }
         }
+        std::vector<int32_t>().swap(pos_of_row);
         std::vector<int32_t> ident(n);
         for (int32_t i = 0; i < n; ++i) ident[i] = i;
-        const long long h0 = window_reuse(S, ident), h1 = window_reuse(S, order);
-        if ((double)h1 < GATHER_REORDER_GAIN * (double)h0 || h1 == h0) return;
-        std::vector<int32_t> rid, rptr(1, 0), col;
-        std::vector<char> val;
-        rid.reserve(n);
-        rptr.reserve((size_t)n + 1);
-        col.reserve(S.ccol.size());
-        val.reserve(S.cval.size());
-        for (int32_t i : order) {
-            rid.push_back(S.crow_id[i]);
-            col.insert(col.end(), S.ccol.begin() + S.crow_ptr[i], S.ccol.begin() + S.crow_ptr[i + 1]);
-            val.insert(val.end(), S.cval.begin() + (size_t)S.crow_ptr[i] * sizeof(T),
-                       S.cval.begin() + (size_t)S.crow_ptr[i + 1] * sizeof(T));
-            rptr.push_back((int32_t)col.size());
+        double h0 = 0.0, h1 = 0.0;
+        {
+            std::vector<int32_t> last0((size_t)in_.cols), last1((size_t)in_.cols);
+            std::thread th([&]() { h1 = window_reuse(S, order, last1); });
+            h0 = window_reuse(S, ident, last0);
+            th.join();
         }
+        if (h1 < GATHER_REORDER_GAIN * h0 || h1 == h0) return;
+        std::vector<int32_t> rid((size_t)n), rptr((size_t)n + 1), col(S.ccol.size());
+        std::vector<char> val(S.cval.size());
+        rptr[0] = 0;
+        for (int32_t p = 0; p < n; ++p) {
+            const int32_t i = order[(size_t)p];
+            rid[(size_t)p] = S.crow_id[(size_t)i];
+            rptr[(size_t)p + 1] = rptr[(size_t)p] + (S.crow_ptr[(size_t)i + 1] - S.crow_ptr[(size_t)i]);
+        }
+        par_ranges((size_t)n, [&](size_t p0, size_t p1) {
+            for (size_t p = p0; p < p1; ++p) {
+                const int32_t i = order[p];
+                const int32_t len = S.crow_ptr[(size_t)i + 1] - S.crow_ptr[(size_t)i];
+                std::memcpy(col.data() + rptr[p], S.ccol.data() + S.crow_ptr[(size_t)i], (size_t)len * 4);
+                std::memcpy(val.data() + (size_t)rptr[p] * sizeof(T),
+                            S.cval.data() + (size_t)S.crow_ptr[(size_t)i] * sizeof(T), (size_t)len * sizeof(T));
+            }
+        });
         S.crow_id.swap(rid);
         S.crow_ptr.swap(rptr);
         S.ccol.swap(col);
