@@ -744,6 +744,49 @@ __device__ __forceinline__ void dma_serial(uint64_t busy, int& rs0, int& rs1, Nz
     }
 }
 
+// Store an item's rows with 4 lanes per row.  Lane 2r + h holds chunks
+// 2q + h (16 bytes each) of row r, so stores straight from registers write
+// 32 bytes to each of 32 rows per instruction.  The quad of lanes 4m .. 4m+3
+// holds rows 2m and 2m+1; swapping one register per chunk pair between lanes
+// i and i ^ 2 (DPP quad_perm) gives lane i, for store 2s, chunk 4s + i of row
+// 2m and, for store 2s + 1, chunk 4s + i of row 2m + 1, so every store
+// instruction writes 64 contiguous bytes to each of 16 rows: half the write
+// requests (cfg2 62.8 -> 61.1 us, cfg1 18.3 -> 16.9 us).  A second exchange
+// between lanes j and j ^ 4 for whole 128-byte lines cost more than it saved
+// (61.5 and 17.3 us).
+__device__ __forceinline__ void dma_store_rows(const StreamArgs<float>& a, const float (&acc)[8][4], int row,
+                                               int slot, int nrow, int b, int fbase) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const int lane = threadIdx.x & 63;
+    const int i = lane & 3;
+    const bool hi = (lane & 2) != 0;
+    const int m2 = (lane >> 2) * 2;                                         // the quad's first local row
+    const int ra = __builtin_amdgcn_mov_dpp(row, 0x00, 0xF, 0xF, false);   // row 2m's id (quad lane 0)
+    const int rb = __builtin_amdgcn_mov_dpp(row, 0xAA, 0xF, 0xF, false);   // row 2m+1's id (quad lane 2)
+    float* oa;
+    float* ob;
+    if (slot < 0) {
+        oa = opaque_ptr(a.Y) + ((size_t)b * a.rows + ra) * a.K + fbase + i * 4;
+        ob = opaque_ptr(a.Y) + ((size_t)b * a.rows + rb) * a.K + fbase + i * 4;
+    } else {
+        oa = opaque_ptr(a.P) + (((size_t)slot * a.batch + b) * ST_ROWS + m2) * a.K + fbase + i * 4;
+        ob = oa + a.K;
+    }
+    const bool wa = m2 < nrow, wb = m2 + 1 < nrow;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        f4 own, rcv;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            own[u] = hi ? acc[2 * s + 1][u] : acc[2 * s][u];
+            const float snd = hi ? acc[2 * s][u] : acc[2 * s + 1][u];
+            rcv[u] = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(snd), 0x4E, 0xF, 0xF, false));  // lane ^ 2
+        }
+        if (wa) *reinterpret_cast<f4*>(oa + 16 * s) = hi ? rcv : own;
+        if (wb) *reinterpret_cast<f4*>(ob + 16 * s) = hi ? own : rcv;
+    }
+}
+
 // WG waves (2 or 4) share each X tile: the tile's 8 DMA instructions are
 // split 8/WG per wave.
 template <int DF, int WG>
@@ -853,7 +896,7 @@ __global__ void __launch_bounds__(64 * WG, SPMM_BOO_DMA_OCC) boo_stream_dma_kern
         wave_lds_fence();
         if (real && ((mt.y >> 24) & ST_FLAG_LAST)) {
             const int nrow = (mt.y >> 16) & 0xff;
-            st_store<float, 32, 4, true>(a, acc, row, slot, nrow, b, fbase);
+            dma_store_rows(a, acc, row, slot, nrow, b, fbase);
 #pragma unroll
             for (int q = 0; q < 8; ++q)
 #pragma unroll
