@@ -21,7 +21,8 @@
 //  * boo_stream_dma_kernel -- the same walk for float 64-feature tiles, with
 //    each wave's share of the next X tile copied from memory straight into
 //    LDS by global_load_lds_dwordx4 (no staging registers), whole X rows per
-//    instruction.
+//    instruction; an item's Y rows are stored 4 lanes per row (64-byte runs)
+//    after a DPP exchange inside each quad of lanes.
 //  * boo_rows_kernel, gather_chunk_kernel, gather_fix_kernel -- the gather
 //    pass: rows whose columns are too scattered for X tiles, a lane group per
 //    row gathering X rows directly; rows over the long-row threshold in
@@ -648,7 +649,8 @@ __global__ void __launch_bounds__(64 * WG, sizeof(T) == 8 && F >= 16 ? 2 : 4) bo
 // feature rows, 16 neighbouring lanes per row, so it reads 8 whole lines; its
 // 1 KiB block starts at I * DMA_BLK, and the 32 bytes of padding per block put
 // columns that differ mod 8 on distinct banks.  Lane (r, h) reads the 8
-// chunks 2m+h of a column at one base plus 32-byte immediates.
+// chunks 2m+h of a column at one base plus 32-byte immediates.  Y rows leave
+// through dma_store_rows (4 lanes per row).
 // ---------------------------------------------------------------------------
 
 #ifndef SPMM_BOO_DMA_HALVES
