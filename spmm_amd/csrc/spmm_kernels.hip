@@ -21,8 +21,8 @@
 //  * boo_stream_dma_kernel -- the same walk for float 64-feature tiles, with
 //    each wave's share of the next X tile copied from memory straight into
 //    LDS by global_load_lds_dwordx4 (no staging registers), whole X rows per
-//    instruction; an item's Y rows are stored 4 lanes per row (64-byte runs)
-//    after a DPP exchange inside each quad of lanes.
+//    instruction.  Both stream kernels store an item's Y rows 4 lanes per row
+//    (64-byte runs) after a DPP exchange inside each quad of lanes.
 //  * boo_rows_kernel, gather_chunk_kernel, gather_fix_kernel -- the gather
 //    pass: rows whose columns are too scattered for X tiles, a lane group per
 //    row gathering X rows directly; rows over the long-row threshold in
@@ -461,6 +461,66 @@ __device__ __forceinline__ void st_store(const StreamArgs<T>& a, const T (&acc)[
     }
 }
 
+// One element moved from lane i ^ 2 of its quad (DPP quad_perm(2,3,0,1)),
+// 32 bits at a time.
+__device__ __forceinline__ float quad_xor2(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+}
+__device__ __forceinline__ double quad_xor2(double v) {
+    const long long w = __builtin_bit_cast(long long, v);
+    const int lo = __builtin_amdgcn_mov_dpp((int)(unsigned)(w & 0xffffffffll), 0x4E, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_mov_dpp((int)(w >> 32), 0x4E, 0xF, 0xF, false);
+    return __builtin_bit_cast(double, ((long long)hi << 32) | (long long)(unsigned)lo);
+}
+
+// st_store with 4 lanes per row, for 16-byte chunks (VEC * sizeof(T) = 16)
+// and an even number of chunks per lane.  Lane 2r + h holds chunks 2q + h of
+// row r, so plain stores write 32 bytes to each of 32 rows per instruction.
+// The quad of lanes 4m .. 4m+3 holds rows 2m and 2m+1; swapping one chunk of
+// each pair (2s, 2s + 1) between lanes i and i ^ 2 (DPP quad_perm) gives lane
+// i chunk 4s + i of row 2m (store 2s) and of row 2m + 1 (store 2s + 1), so
+// every store instruction writes 64 contiguous bytes to each of 16 rows: half
+// the write requests (config 2 62.8 -> 61.1 us, config 1 18.3 -> 16.9 us).  A
+// second exchange between lanes j and j ^ 4 for whole 128-byte lines cost
+// more than it saved (61.5 and 17.3 us).
+template <typename T, int F, int VEC, bool FULL>
+__device__ __forceinline__ void st_store_quad(const StreamArgs<T>& a, const T (&acc)[F / VEC][VEC], int row,
+                                              int slot, int nrow, int b, int fbase) {
+    static_assert(VEC * sizeof(T) == 16 && (F / VEC) % 2 == 0, "16-byte chunks, an even number per lane");
+    constexpr int NQ = F / VEC;
+    const int lane = threadIdx.x & 63;
+    const int i = lane & 3;
+    const bool hi = (lane & 2) != 0;
+    const int m2 = (lane >> 2) * 2;                                         // the quad's first local row
+    const int ra = __builtin_amdgcn_mov_dpp(row, 0x00, 0xF, 0xF, false);   // row 2m's id (quad lane 0)
+    const int rb = __builtin_amdgcn_mov_dpp(row, 0xAA, 0xF, 0xF, false);   // row 2m+1's id (quad lane 2)
+    const int K = a.K;
+    T* oa;
+    T* ob;
+    if (slot < 0) {
+        oa = opaque_ptr(a.Y) + ((size_t)b * a.rows + ra) * K + fbase + i * VEC;
+        ob = opaque_ptr(a.Y) + ((size_t)b * a.rows + rb) * K + fbase + i * VEC;
+    } else {
+        oa = opaque_ptr(a.P) + (((size_t)slot * a.batch + b) * ST_ROWS + m2) * K + fbase + i * VEC;
+        ob = oa + K;
+    }
+    const bool wa = m2 < nrow, wb = m2 + 1 < nrow;
+#pragma unroll
+    for (int s = 0; s < NQ / 2; ++s) {
+        T own[VEC], rcv[VEC], da[VEC], db[VEC];
+#pragma unroll
+        for (int u = 0; u < VEC; ++u) {
+            own[u] = hi ? acc[2 * s + 1][u] : acc[2 * s][u];
+            rcv[u] = quad_xor2(hi ? acc[2 * s][u] : acc[2 * s + 1][u]);
+            da[u] = hi ? rcv[u] : own[u];   // chunk 4s + i of row 2m
+            db[u] = hi ? own[u] : rcv[u];   // chunk 4s + i of row 2m + 1
+        }
+        if (!FULL && fbase + (4 * s + i) * VEC >= K) continue;
+        if (wa) store_vec<T, VEC>(oa + 4 * s * VEC, da);
+        if (wb) store_vec<T, VEC>(ob + 4 * s * VEC, db);
+    }
+}
+
 // LDS of one workgroup of WG waves: the shared X tile, double-buffered, and
 // per wave its entries, its serial-row sums and its column ids.
 template <typename T, int F, int VEC, int WG>
@@ -622,7 +682,10 @@ __global__ void __launch_bounds__(64 * WG, sizeof(T) == 8 && F >= 16 ? 2 : 4) bo
         // (4) end of the item: store its rows
         if (real && ((mt.y >> 24) & ST_FLAG_LAST)) {
             const int nrow = (mt.y >> 16) & 0xff;
-            st_store<T, F, VEC, FULL>(a, acc, row, slot, nrow, b, fbase);
+            if constexpr (VEC * sizeof(T) == 16 && (F / VEC) % 2 == 0)
+                st_store_quad<T, F, VEC, FULL>(a, acc, row, slot, nrow, b, fbase);
+            else
+                st_store<T, F, VEC, FULL>(a, acc, row, slot, nrow, b, fbase);
 #pragma unroll
             for (int q = 0; q < G::NQ; ++q)
 #pragma unroll
@@ -650,7 +713,7 @@ __global__ void __launch_bounds__(64 * WG, sizeof(T) == 8 && F >= 16 ? 2 : 4) bo
 // 1 KiB block starts at I * DMA_BLK, and the 32 bytes of padding per block put
 // columns that differ mod 8 on distinct banks.  Lane (r, h) reads the 8
 // chunks 2m+h of a column at one base plus 32-byte immediates.  Y rows leave
-// through dma_store_rows (4 lanes per row).
+// through st_store_quad (4 lanes per row).
 // ---------------------------------------------------------------------------
 
 #ifndef SPMM_BOO_DMA_HALVES
@@ -743,49 +806,6 @@ __device__ __forceinline__ void dma_serial(uint64_t busy, int& rs0, int& rs1, Nz
             rs0 = ST_ENT + k;
             rs1 = ST_ENT + k + 1;
         }
-    }
-}
-
-// Store an item's rows with 4 lanes per row.  Lane 2r + h holds chunks
-// 2q + h (16 bytes each) of row r, so stores straight from registers write
-// 32 bytes to each of 32 rows per instruction.  The quad of lanes 4m .. 4m+3
-// holds rows 2m and 2m+1; swapping one register per chunk pair between lanes
-// i and i ^ 2 (DPP quad_perm) gives lane i, for store 2s, chunk 4s + i of row
-// 2m and, for store 2s + 1, chunk 4s + i of row 2m + 1, so every store
-// instruction writes 64 contiguous bytes to each of 16 rows: half the write
-// requests (cfg2 62.8 -> 61.1 us, cfg1 18.3 -> 16.9 us).  A second exchange
-// between lanes j and j ^ 4 for whole 128-byte lines cost more than it saved
-// (61.5 and 17.3 us).
-__device__ __forceinline__ void dma_store_rows(const StreamArgs<float>& a, const float (&acc)[8][4], int row,
-                                               int slot, int nrow, int b, int fbase) {
-    typedef float f4 __attribute__((ext_vector_type(4)));
-    const int lane = threadIdx.x & 63;
-    const int i = lane & 3;
-    const bool hi = (lane & 2) != 0;
-    const int m2 = (lane >> 2) * 2;                                         // the quad's first local row
-    const int ra = __builtin_amdgcn_mov_dpp(row, 0x00, 0xF, 0xF, false);   // row 2m's id (quad lane 0)
-    const int rb = __builtin_amdgcn_mov_dpp(row, 0xAA, 0xF, 0xF, false);   // row 2m+1's id (quad lane 2)
-    float* oa;
-    float* ob;
-    if (slot < 0) {
-        oa = opaque_ptr(a.Y) + ((size_t)b * a.rows + ra) * a.K + fbase + i * 4;
-        ob = opaque_ptr(a.Y) + ((size_t)b * a.rows + rb) * a.K + fbase + i * 4;
-    } else {
-        oa = opaque_ptr(a.P) + (((size_t)slot * a.batch + b) * ST_ROWS + m2) * a.K + fbase + i * 4;
-        ob = oa + a.K;
-    }
-    const bool wa = m2 < nrow, wb = m2 + 1 < nrow;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-        f4 own, rcv;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            own[u] = hi ? acc[2 * s + 1][u] : acc[2 * s][u];
-            const float snd = hi ? acc[2 * s][u] : acc[2 * s + 1][u];
-            rcv[u] = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(snd), 0x4E, 0xF, 0xF, false));  // lane ^ 2
-        }
-        if (wa) *reinterpret_cast<f4*>(oa + 16 * s) = hi ? rcv : own;
-        if (wb) *reinterpret_cast<f4*>(ob + 16 * s) = hi ? own : rcv;
     }
 }
 
@@ -898,7 +918,7 @@ __global__ void __launch_bounds__(64 * WG, SPMM_BOO_DMA_OCC) boo_stream_dma_kern
         wave_lds_fence();
         if (real && ((mt.y >> 24) & ST_FLAG_LAST)) {
             const int nrow = (mt.y >> 16) & 0xff;
-            dma_store_rows(a, acc, row, slot, nrow, b, fbase);
+            st_store_quad<float, 32, 4, true>(a, acc, row, slot, nrow, b, fbase);
 #pragma unroll
             for (int q = 0; q < 8; ++q)
 #pragma unroll
