@@ -138,6 +138,25 @@ __device__ __forceinline__ void load_vec(const T* p, T (&out)[VEC]) {
     }
 }
 
+// store_vec through a global (address space 1) pointer: a global store,
+// tracked by the vector-memory counter alone.  A flat store -- what a generic
+// pointer the compiler cannot trace to a kernel argument becomes -- also
+// holds the LDS counter until it is acknowledged, so the next wait for an
+// LDS read would wait for the store too.
+template <typename T, int VEC>
+__device__ __forceinline__ void store_vec_global(T* p, const T (&in)[VEC]) {
+    typedef typename Vec<T, VEC>::type V;
+    typedef __attribute__((address_space(1))) V gV;
+    V v;
+    if constexpr (VEC == 1) {
+        v = in[0];
+    } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) v[e] = in[e];
+    }
+    *(gV*)(p) = v;
+}
+
 template <typename T, int VEC>
 __device__ __forceinline__ void store_vec(T* p, const T (&in)[VEC]) {
     typedef typename Vec<T, VEC>::type V;
@@ -457,7 +476,7 @@ __device__ __forceinline__ void st_store(const StreamArgs<T>& a, const T (&acc)[
                           : opaque_ptr(a.P) + (((size_t)slot * a.batch + b) * ST_ROWS + lr) * K + fbase + h * VEC;
 #pragma unroll
         for (int q = 0; q < G::NQ; ++q)
-            if (FULL || fbase + (2 * q + h) * VEC < K) store_vec<T, VEC>(out + 2 * q * VEC, acc[q]);
+            if (FULL || fbase + (2 * q + h) * VEC < K) store_vec_global<T, VEC>(out + 2 * q * VEC, acc[q]);
     }
 }
 
@@ -516,8 +535,8 @@ __device__ __forceinline__ void st_store_quad(const StreamArgs<T>& a, const T (&
             db[u] = hi ? own[u] : rcv[u];   // chunk 4s + i of row 2m + 1
         }
         if (!FULL && fbase + (4 * s + i) * VEC >= K) continue;
-        if (wa) store_vec<T, VEC>(oa + 4 * s * VEC, da);
-        if (wb) store_vec<T, VEC>(ob + 4 * s * VEC, db);
+        if (wa) store_vec_global<T, VEC>(oa + 4 * s * VEC, da);
+        if (wb) store_vec_global<T, VEC>(ob + 4 * s * VEC, db);
     }
 }
 
