@@ -115,6 +115,7 @@ typedef struct spmm_boo_stage_info {
     int32_t n_slots, n_waves, group, n_crow_long;
     int32_t n_stream_rows;       /* rows the tile stream stores; n_stream_rows + n_crow == rows */
     int64_t n_blob16;            /* record stream length in 16-byte units (0: none) */
+    int64_t n_gtask_order;       /* chunk-task launch order length: 0 (task order) or n_gtask */
 } spmm_boo_stage_info;
 
 /* group (1, 2 or 4): slices that share column chunks are put together, up to
@@ -158,6 +159,14 @@ int spmm_boo_stage_copy(const spmm_boo_stage* st, int32_t* tiles, uint16_t* tile
  * Optional: a descriptor without it runs the same tiles through the other
  * kernels (same results within the stated tolerance). */
 int spmm_boo_stage_copy_blobs(const spmm_boo_stage* st, void* blobs, uint32_t* blob_first, uint32_t* blob_xid);
+/* The launch order of the chunk tasks when it is not task order
+ * (n_gtask_order = n_gtask > 0): gtask_order [n_gtask] int32, a permutation of
+ * the task ids.  A power-law matrix's long rows are split into tasks over
+ * their entries in the most used columns and tasks over the rest, and every
+ * task of the first kind runs first, so those columns' X rows stay in L2.
+ * Optional: a descriptor without it runs the tasks in task order (same
+ * results: each row's partial rows are added in task order either way). */
+int spmm_boo_stage_copy_gtask_order(const spmm_boo_stage* st, int32_t* gtask_order);
 void spmm_boo_stage_destroy(spmm_boo_stage* st);
 
 /* Device descriptor: the staged arrays plus row_ids and the remainder CSR
@@ -200,6 +209,7 @@ typedef struct spmm_boo_desc {
     const void* blobs;           /* [n_blob16*16] bytes */
     const uint32_t* blob_first;  /* [n_waves*8] */
     const uint32_t* blob_xid;    /* [n_tiles*8] */
+    const int32_t* gtask_order;  /* [n_gtask] launch order of the chunk tasks, or NULL: task order */
 } spmm_boo_desc;
 
 /* Workspace bytes spmm_boo_matmul needs for this staging and shape: the

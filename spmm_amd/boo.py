@@ -218,6 +218,9 @@ def _kernel_staging(rows, cols, d, rowmajor, row_ids_dev, device, rem_dev=None):
     records = RECORD_STREAM and int(stage['n_blob16']) > 0
     if records:
         names += ['blobs', 'blob_first', 'blob_xid']
+    ordered = int(stage['n_gtask_order']) > 0   # hot-column chunk tasks first
+    if ordered:
+        names += ['gtask_order']
     g = types.SimpleNamespace(**{k: _pinned(stage[k], device) for k in names})
     if rem_dev is None:
         rem_dev = (_pinned(k_rem_indptr, device), _pinned(k_rem_col, device), _pinned(k_rem_val, device))
@@ -239,6 +242,7 @@ def _kernel_staging(rows, cols, d, rowmajor, row_ids_dev, device, rem_dev=None):
         'n_blob16': int(stage['n_blob16']) if records else 0,
         'blobs': p(g.blobs) if records else 0, 'blob_first': p(g.blob_first) if records else 0,
         'blob_xid': p(g.blob_xid) if records else 0,
+        'gtask_order': p(g.gtask_order) if ordered else 0,
     }
     return g, rem_dev, desc
 

@@ -71,6 +71,21 @@ constexpr int GATHER_CHUNK = 1024;
 // lengths the chunks' partial rows and fixup cost more than they save (48
 // entries per row: 248 -> 423 us at K=32), so the threshold stays as given.
 constexpr int GATHER_SKEWED_LONG = 32;
+// Chunk tasks read X rows at random from every column, and on a power-law
+// graph a few columns carry much of the entries, yet in one pass their X rows
+// keep being evicted from L2 by the cold gathers in between (R-MAT 2^20: the
+// 16,384 most used columns carry 55 % of the entries, the chunk pass hits L2
+// on ~40 % of its reads).  When the GATHER_HOT_COLS most used columns of the
+// long gather rows carry at least GATHER_HOT_SHARE of their entries (and
+// GATHER_HOT_SKEW times their share of the columns), each long row's entries
+// in those columns come first, in their own chunk tasks, and every such task
+// is launched before the others: their X rows -- 256 bytes of each per
+// workgroup's feature slab, 4 MiB for 16,384 of them, one XCD's L2 -- then
+// stay resident while they run.  Each row's partial rows are still added in
+// its task order, so its sum is deterministic.
+constexpr int GATHER_HOT_COLS = 16384;
+constexpr double GATHER_HOT_SHARE = 0.25;
+constexpr double GATHER_HOT_SKEW = 4.0;
 // The gather pass walks its short rows in staging order, and rows next to
 // each other in that order run at about the same time on one XCD, so X rows
 // they share are fetched once into that XCD's L2.  When a Cuthill-McKee order
@@ -134,6 +149,9 @@ struct Staged {
     int32_t n_crow_long = 0;
     std::vector<int32_t> gtask;      // [n_gtask][2]
     std::vector<int32_t> gtask_ptr;  // [n_crow_long+1]
+    // launch order of the chunk tasks (hot-column tasks first), or empty:
+    // task order
+    std::vector<int32_t> gtask_order;
     int32_t n_slots = 0;
     int32_t n_waves = 0;
     int32_t group = 1;               // waves per workgroup sharing X tiles
@@ -543,21 +561,87 @@ private:
         std::vector<T>().swap(short_val);
         reorder_short_rows(S);
         S.n_crow_long = (int32_t)long_id.size();
+        std::vector<int32_t> n_hot;  // per long row: entries in hot columns (empty: no split)
+        hot_first(long_ptr, long_col, long_val, n_hot);
         S.gtask_ptr.assign(1, 0);
+        S.gtask_order.clear();
+        std::vector<int32_t> cold_tasks;
         const int32_t base = (int32_t)S.ccol.size();
+        auto cut = [&](int32_t e0, int32_t e1, std::vector<int32_t>* order) {
+            for (int32_t e = e0; e < e1; e += GATHER_CHUNK) {
+                if (order) order->push_back((int32_t)(S.gtask.size() / 2));
+                S.gtask.push_back(base + e);
+                S.gtask.push_back(base + std::min(e1, e + GATHER_CHUNK));
+            }
+        };
         for (size_t i = 0; i < long_id.size(); ++i) {
             S.crow_id.push_back(long_id[i]);
-            for (int32_t e = long_ptr[i]; e < long_ptr[i + 1]; e += GATHER_CHUNK) {
-                S.gtask.push_back(base + e);
-                S.gtask.push_back(base + std::min(long_ptr[i + 1], e + GATHER_CHUNK));
+            if (n_hot.empty()) {
+                cut(long_ptr[i], long_ptr[i + 1], nullptr);
+            } else {
+                const int32_t ph = long_ptr[i] + n_hot[i];
+                cut(long_ptr[i], ph, &S.gtask_order);
+                cut(ph, long_ptr[i + 1], &cold_tasks);
             }
             S.gtask_ptr.push_back((int32_t)(S.gtask.size() / 2));
             S.crow_ptr.push_back(base + long_ptr[i + 1]);
         }
+        S.gtask_order.insert(S.gtask_order.end(), cold_tasks.begin(), cold_tasks.end());
         S.ccol.insert(S.ccol.end(), long_col.begin(), long_col.end());
         const size_t v0 = S.cval.size();
         S.cval.resize(v0 + long_val.size() * sizeof(T));
         if (!long_val.empty()) std::memcpy(S.cval.data() + v0, long_val.data(), long_val.size() * sizeof(T));
+    }
+
+    // The hot-column split of the long gather rows (see GATHER_HOT_COLS): if
+    // the matrix qualifies, each row's entries in the hot columns are moved
+    // to its front (both parts keep their order) and n_hot gets each row's
+    // count of them; otherwise n_hot is left empty.
+    void hot_first(const std::vector<int32_t>& ptr, std::vector<int32_t>& col, std::vector<T>& val,
+                   std::vector<int32_t>& n_hot) const {
+        n_hot.clear();
+        const size_t nrow = ptr.empty() ? 0 : ptr.size() - 1;
+        const int32_t cols = in_.cols;
+        if (nrow == 0 || col.empty() || cols <= GATHER_HOT_COLS) return;
+        std::vector<int32_t> cnt((size_t)cols, 0);
+        for (int32_t c : col) ++cnt[(size_t)c];
+        // the GATHER_HOT_COLS most used columns (ties: lower column first)
+        std::vector<int32_t> ids((size_t)cols);
+        for (int32_t c = 0; c < cols; ++c) ids[(size_t)c] = c;
+        auto more_used = [&](int32_t a, int32_t b) { return cnt[(size_t)a] != cnt[(size_t)b] ? cnt[(size_t)a] > cnt[(size_t)b] : a < b; };
+        std::nth_element(ids.begin(), ids.begin() + (GATHER_HOT_COLS - 1), ids.end(), more_used);
+        std::vector<uint8_t> hot((size_t)cols, 0);
+        long long n_in = 0;
+        for (int k = 0; k < GATHER_HOT_COLS; ++k) {
+            hot[(size_t)ids[(size_t)k]] = 1;
+            n_in += cnt[(size_t)ids[(size_t)k]];
+        }
+        const double share = (double)n_in / (double)col.size();
+        if (share < GATHER_HOT_SHARE || share < GATHER_HOT_SKEW * GATHER_HOT_COLS / (double)cols) return;
+        n_hot.assign(nrow, 0);
+        par_ranges(nrow, [&](size_t r0, size_t r1) {
+            std::vector<int32_t> tc;
+            std::vector<T> tv;
+            for (size_t i = r0; i < r1; ++i) {
+                const size_t p0 = (size_t)ptr[i], p1 = (size_t)ptr[i + 1];
+                tc.clear();
+                tv.clear();
+                size_t q = p0;
+                for (size_t p = p0; p < p1; ++p) {
+                    if (hot[(size_t)col[p]]) {
+                        col[q] = col[p];
+                        val[q] = val[p];
+                        ++q;
+                    } else {
+                        tc.push_back(col[p]);
+                        tv.push_back(val[p]);
+                    }
+                }
+                n_hot[i] = (int32_t)(q - p0);
+                std::copy(tc.begin(), tc.end(), col.begin() + (std::ptrdiff_t)q);
+                std::copy(tv.begin(), tv.end(), val.begin() + (std::ptrdiff_t)q);
+            }
+        });
     }
 
     // Entries among the first GATHER_REUSE_SAMPLE entries of the short gather

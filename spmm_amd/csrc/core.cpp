@@ -305,6 +305,7 @@ spmm_boo_desc boo_desc(const py::dict& d) {
         A.blob_first = reinterpret_cast<const uint32_t*>(P(d, "blob_first"));
         A.blob_xid = reinterpret_cast<const uint32_t*>(P(d, "blob_xid"));
     }
+    if (d.contains("gtask_order")) A.gtask_order = reinterpret_cast<const int32_t*>(P(d, "gtask_order"));
     return A;
 }
 
@@ -359,10 +360,15 @@ py::dict boo_stage(const py::dict& h, int32_t max_item_nnz, int32_t long_thresho
     std::vector<uint32_t> blobs((size_t)inf.n_blob16 * 4), bfirst(inf.n_blob16 > 0 ? (size_t)inf.n_waves * 8 : 0),
         bxid(inf.n_blob16 > 0 ? (size_t)inf.n_tiles * 8 : 0);
     const int rc2 = rc ? rc : spmm_boo_stage_copy_blobs(st, blobs.data(), bfirst.data(), bxid.data());
+    std::vector<int32_t> gord((size_t)inf.n_gtask_order);
+    const int rc3 = rc2 ? rc2 : spmm_boo_stage_copy_gtask_order(st, gord.data());
     spmm_boo_stage_destroy(st);
     raise_status(rc);
     raise_status(rc2);
+    raise_status(rc3);
     py::dict d;
+    d["gtask_order"] = give(std::move(gord));
+    d["n_gtask_order"] = inf.n_gtask_order;
     d["blobs"] = give(std::move(blobs));
     d["blob_first"] = give(std::move(bfirst));
     d["blob_xid"] = give(std::move(bxid));

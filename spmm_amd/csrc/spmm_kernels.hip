@@ -1346,16 +1346,21 @@ __global__ void __launch_bounds__(256) boo_rows_kernel(const int* __restrict__ c
 // Long gather rows: one workgroup per chunk task (at most a fixed number of
 // one row's entries), 16 entry slots x 16 lanes of VEC features, U entries per
 // slot in flight; the slots' sums are reduced in a fixed order through LDS
-// into the task's partial row P[task][b][:].
+// into the task's partial row P[task][b][:].  Workgroup x of a feature slab
+// runs task order[x] (null: task x): the staging puts the tasks over a
+// power-law matrix's most used columns first, and the workgroups are
+// dispatched x first, so within each feature slab those tasks run together
+// while their X rows fit in L2.
 template <typename T, int VEC>
 __global__ void __launch_bounds__(256) gather_chunk_kernel(const int* __restrict__ gtask,
+                                                           const int* __restrict__ order,
                                                            const int* __restrict__ ccol,
                                                            const T* __restrict__ cval,
                                                            const T* __restrict__ X, T* __restrict__ P,
                                                            int cols, int K, int batch) {
     constexpr int LANES = 16, SLOTS = 16, KT = LANES * VEC, U = 4;
     __shared__ T red[SLOTS][KT];
-    const int t = blockIdx.x;
+    const int t = order ? order[blockIdx.x] : (int)blockIdx.x;  // launch position -> task
     const int b = blockIdx.z;
     const int slot = threadIdx.x / LANES;
     const int ch = threadIdx.x % LANES;
@@ -1931,10 +1936,10 @@ int launch_boo_rows(const spmm_boo_desc* A, const T* X, T* Y, int K, int batch, 
     if (A->n_gtask > 0) {
         const int v = vec ? V : 1;
         const dim3 grid(A->n_gtask, (K + 16 * v - 1) / (16 * v), batch);
-        rc = vec ? launch("gather_chunk_kernel", gather_chunk_kernel<T, V>, grid, dim3(256), s, A->gtask, A->ccol,
-                          static_cast<const T*>(A->cval), X, P2, A->cols, K, batch)
-                 : launch("gather_chunk_kernel", gather_chunk_kernel<T, 1>, grid, dim3(256), s, A->gtask, A->ccol,
-                          static_cast<const T*>(A->cval), X, P2, A->cols, K, batch);
+        rc = vec ? launch("gather_chunk_kernel", gather_chunk_kernel<T, V>, grid, dim3(256), s, A->gtask,
+                          A->gtask_order, A->ccol, static_cast<const T*>(A->cval), X, P2, A->cols, K, batch)
+                 : launch("gather_chunk_kernel", gather_chunk_kernel<T, 1>, grid, dim3(256), s, A->gtask,
+                          A->gtask_order, A->ccol, static_cast<const T*>(A->cval), X, P2, A->cols, K, batch);
         if (rc) return rc;
     }
     return launch("gather_fix_kernel", gather_fix_kernel<T>, dim3(A->n_crow_long, 1, batch), dim3(256), s,
@@ -2241,6 +2246,7 @@ int spmm_boo_stage_sizes(const spmm_boo_stage* st, spmm_boo_stage_info* info) {
     info->n_stream_rows = st->s.n_stream_rows;
     info->n_blob16 = (int64_t)(st->s.blobs.size() / 4);
     info->n_gtask = (int64_t)(st->s.gtask.size() / 2);
+    info->n_gtask_order = (int64_t)st->s.gtask_order.size();
     info->n_slots = st->s.n_slots;
     info->n_waves = st->s.n_waves;
     info->group = st->s.group;
@@ -2282,6 +2288,15 @@ int spmm_boo_stage_copy_blobs(const spmm_boo_stage* st, void* blobs, uint32_t* b
     std::memcpy(blobs, s.blobs.data(), s.blobs.size() * 4);
     std::memcpy(blob_first, s.blob_first.data(), s.blob_first.size() * 4);
     std::memcpy(blob_xid, s.blob_xid.data(), s.blob_xid.size() * 4);
+    return SPMM_OK;
+}
+
+int spmm_boo_stage_copy_gtask_order(const spmm_boo_stage* st, int32_t* gtask_order) {
+    if (!st) return fail(SPMM_EINVAL, "null staging handle");
+    const spmm_stage::Staged& s = st->s;
+    if (s.gtask_order.empty()) return SPMM_OK;
+    if (!gtask_order) return fail(SPMM_EINVAL, "null output array for the chunk-task order");
+    std::memcpy(gtask_order, s.gtask_order.data(), s.gtask_order.size() * 4);
     return SPMM_OK;
 }
 

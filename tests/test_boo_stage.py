@@ -78,7 +78,9 @@ def check_stream(A, boo, max_item_nnz=4096, long_thr=256, n_waves=64, group=1, m
     want = sp.csr_matrix((np.ones(A.nnz, np.int64), A.indices, A.indptr), shape=A.shape)
     assert (got != want).nnz == 0
     B = sp.coo_matrix((v, (r, c)), shape=A.shape).tocsr()
-    assert np.array_equal(B.toarray(), A.toarray())
+    D = (B - A).tocsr()
+    D.eliminate_zeros()
+    assert D.nnz == 0                                  # and each with its own value
     # items / waves
     tiles = st['tiles'].reshape(-1, 8)
     last = (tiles[:, 1] >> 24) & 1
@@ -313,6 +315,54 @@ def test_gather_pass_skewed_rows_chunk_earlier():
     boo = S.csr_to_boo(E, cluster='identity', target_nr=32, target_nc=32)
     st = check_stream(E, boo, long_thr=256, min_reuse=1.5, group=4)
     assert len(st['crow_id']) == n and st['n_crow_long'] == 0
+
+
+def _hot_columns(ccol, n_cols, n_hot):
+    """The n_hot most used columns of ccol (ties: lower column first), as a mask."""
+    cnt = np.bincount(ccol, minlength=n_cols)
+    order = np.lexsort((np.arange(n_cols), -cnt))
+    mask = np.zeros(n_cols, bool)
+    mask[order[:n_hot]] = True
+    return mask
+
+
+def test_gather_pass_hot_columns_first():
+    # R-MAT 2^17: the long gather rows' entries in their 16,384 most used
+    # columns become tasks of their own, every one launched before the rest
+    A = M.rmat(scale=17, edge_factor=8, seed=3)
+    boo = S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32)
+    st = check_stream(A, boo, long_thr=256, min_reuse=1.5, group=4)
+    gt = st['gtask'].reshape(-1, 2)
+    go = st['gtask_order']
+    n_long = st['n_crow_long']
+    assert n_long > 1000 and len(go) == len(gt)
+    assert np.array_equal(np.sort(go), np.arange(len(gt)))          # a permutation of the tasks
+    cp = st['crow_ptr']
+    first = cp[len(cp) - 1 - n_long]                                  # the long rows' first entry
+    hot = _hot_columns(st['ccol'][first:], A.shape[1], 16384)
+    kind = np.array([int(hot[st['ccol'][a:b]].all()) - int((~hot[st['ccol'][a:b]]).all()) for a, b in gt])
+    assert np.all(kind != 0)                                          # each task all hot (1) or all cold (-1)
+    n_hot = int((kind == 1).sum())
+    assert 0 < n_hot < len(gt)
+    assert np.all(kind[go[:n_hot]] == 1) and np.all(kind[go[n_hot:]] == -1)
+    # inside a row: its hot tasks, then its cold ones, each part in column order
+    gp = st['gtask_ptr']
+    for i in range(0, n_long, 97):
+        k = kind[gp[i]:gp[i + 1]]
+        assert np.all(np.diff(k) <= 0)
+        a, b = gt[gp[i], 0], gt[gp[i + 1] - 1, 1]
+        h = hot[st['ccol'][a:b]]
+        assert np.all(np.diff(h.astype(int)) <= 0)
+    # the same shape with columns used evenly: no split, tasks in task order
+    rng = np.random.default_rng(2)
+    n = A.shape[0]
+    lens = np.diff(A.indptr)
+    cols = np.concatenate([rng.choice(n, int(m), replace=False) for m in lens]).astype(np.int32)
+    E = sp.csr_matrix((np.ones(len(cols), np.float32), cols, A.indptr), shape=A.shape)
+    E.sort_indices()
+    st = check_stream(E, S.csr_to_boo(E, cluster='identity', target_nr=32, target_nc=32), long_thr=256,
+                      min_reuse=1.5, group=4)
+    assert st['n_crow_long'] > 1000 and len(st['gtask_order']) == 0
 
 
 def test_gather_rows_reordered_when_it_keeps_x_rows_close():

@@ -41,7 +41,7 @@ class StageInfo(C.Structure):
     _fields_ = [('n_tiles', C.c_int64), ('n_ent', C.c_int64), ('n_tcols', C.c_int64), ('n_splits', C.c_int64),
                 ('n_long', C.c_int64), ('n_crow', C.c_int64), ('n_cnz', C.c_int64), ('n_gtask', C.c_int64),
                 ('n_slots', C.c_int32), ('n_waves', C.c_int32), ('group', C.c_int32), ('n_crow_long', C.c_int32),
-                ('n_stream_rows', C.c_int32), ('n_blob16', C.c_int64)]
+                ('n_stream_rows', C.c_int32), ('n_blob16', C.c_int64), ('n_gtask_order', C.c_int64)]
 
 
 class BooDesc(C.Structure):
@@ -52,7 +52,8 @@ class BooDesc(C.Structure):
                 ('long_rows', P_), ('n_crow', C.c_int32), ('crow_ptr', P_), ('crow_id', P_), ('ccol', P_),
                 ('cval', P_), ('n_crow_long', C.c_int32), ('n_gtask', C.c_int32), ('gtask', P_),
                 ('gtask_ptr', P_), ('rem_indptr', P_), ('rem_col_ind', P_), ('rem_vals', P_),
-                ('n_blob16', C.c_int64), ('blobs', P_), ('blob_first', P_), ('blob_xid', P_)]
+                ('n_blob16', C.c_int64), ('blobs', P_), ('blob_first', P_), ('blob_xid', P_),
+                ('gtask_order', P_)]
 
 
 class PbrDesc(C.Structure):
@@ -109,6 +110,7 @@ def stage_boo_via_c(lib, boo, dev, keep):
         'blobs': np.zeros(n.n_blob16 * 4, np.uint32),
         'blob_first': np.zeros(n.n_waves * 8 if n.n_blob16 else 0, np.uint32),
         'blob_xid': np.zeros(n.n_tiles * 8 if n.n_blob16 else 0, np.uint32),
+        'gtask_order': np.zeros(n.n_gtask_order, i32),
     }
     order = ('tiles', 'tile_rs', 'ent_val', 'ent_col', 'tcols', 'splits', 'long_rows', 'wave_tiles',
              'crow_ptr', 'crow_id', 'ccol', 'cval', 'gtask', 'gtask_ptr')
@@ -116,6 +118,8 @@ def stage_boo_via_c(lib, boo, dev, keep):
     assert rc == 0, lib.spmm_last_error()
     rc = lib.spmm_boo_stage_copy_blobs(st, P_(out['blobs'].ctypes.data), P_(out['blob_first'].ctypes.data),
                                        P_(out['blob_xid'].ctypes.data))
+    assert rc == 0, lib.spmm_last_error()
+    rc = lib.spmm_boo_stage_copy_gtask_order(st, P_(out['gtask_order'].ctypes.data))
     assert rc == 0, lib.spmm_last_error()
     lib.spmm_boo_stage_destroy(st)
     dv = {k: torch.from_numpy(v).to(dev) for k, v in out.items()}
@@ -132,7 +136,7 @@ def stage_boo_via_c(lib, boo, dev, keep):
                    n_gtask=n.n_gtask, gtask=ptr('gtask'), gtask_ptr=ptr('gtask_ptr'),
                    rem_indptr=ptr('rem_indptr'), rem_col_ind=ptr('rem_col_ind'), rem_vals=ptr('rem_vals'),
                    n_blob16=n.n_blob16, blobs=ptr('blobs'), blob_first=ptr('blob_first'),
-                   blob_xid=ptr('blob_xid'))
+                   blob_xid=ptr('blob_xid'), gtask_order=ptr('gtask_order'))
     return desc, n
 
 

@@ -445,3 +445,30 @@ def test_hem_clustered_product(target, shape):
     boo = S.csr_to_boo(A, target_nr=target, target_nc=target).to('cuda')
     x = _x((2, shape[1], 33)).cuda()
     check(S.boo_matmul(boo, x), A, x)
+
+
+def test_hot_column_tasks_first(path):
+    """A power-law graph's long gather rows: the chunk tasks over their most
+    used columns are launched first (gtask_order).  The product is within the
+    bound, and the same staging run in task order gives the same Y bit for
+    bit: each row's partial rows are added in task order either way."""
+    from spmm_amd import matrices as M
+    from spmm_amd._native import core
+    A = M.rmat(scale=17, edge_factor=8, seed=3)
+    K = 64
+    x = torch.from_numpy(np.random.default_rng(1).standard_normal((A.shape[1], K)).astype(np.float32)).cuda()
+    boo = S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32).to('cuda')
+    y = S.boo_matmul(boo, x)
+    check(y, A, x)
+    desc = boo._gpu_meta.desc
+    if path == 'gather':
+        assert desc['gtask_order'] != 0
+    if desc['gtask_order']:
+        plain = dict(desc, gtask_order=0)
+        y2 = torch.empty_like(y)
+        wsb = int(core.boo_workspace_bytes(plain, 0, 1, K))
+        ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device='cuda')
+        core.boo_matmul_gpu(plain, 0, int(x.data_ptr()), int(y2.data_ptr()), 1, K, int(ws.data_ptr()), wsb,
+                            int(torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        assert torch.equal(y, y2)
