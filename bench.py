@@ -336,9 +336,19 @@ def main():
         thr = spec.get('pbr_threshold', 4)
         pbrs = [S.csr_to_pbr(A, 8, 8, thr).to(dev) for _ in range(nrot)]
 
+        # a scattered PBR matrix runs its CSR through the BOO gather pass, as
+        # pbr_matmul does (spmm_amd.pbr.GATHER_MAX_BLOCK_SHARE)
+        gather = pbrs[0]._gpu_meta.gather is not None
+        pws_bytes = int(S._core.boo_workspace_bytes(pbrs[0]._gpu_meta.gather.desc, 0, 1, K)) if gather else 0
+        pws = torch.empty(max(pws_bytes, 1), dtype=torch.uint8, device=dev)
+
         def pbr_step(i):
-            S._core.pbr_matmul_gpu(pbrs[i]._gpu_meta.desc, 0, int(Xs[i].data_ptr()),
-                                   int(Ys[i].data_ptr()), 1, K, int(stream))
+            if gather:
+                S._core.boo_matmul_gpu(pbrs[i]._gpu_meta.gather.desc, 0, int(Xs[i].data_ptr()),
+                                       int(Ys[i].data_ptr()), 1, K, int(pws.data_ptr()), pws_bytes, int(stream))
+            else:
+                S._core.pbr_matmul_gpu(pbrs[i]._gpu_meta.desc, 0, int(Xs[i].data_ptr()),
+                                       int(Ys[i].data_ptr()), 1, K, int(stream))
         pbr_step(0)
         torch.cuda.synchronize()
         y_gpu['pbr'] = Ys[0][0].cpu().numpy()
@@ -349,7 +359,8 @@ def main():
         p_wall, p_ev = time_steps([lambda i=i: pbr_step(i) for i in range(nrot)], args.steps,
                                      args.warmup, torch)
         pbr_workload = f'cfg{args.config}_{spec["name"]}_pbr8x8_thr{thr}_K{K}'
-        pbr = {'ms_per_step': round(p_wall, 5), 'kernel_ms_mean': round(p_ev, 5),
+        pbr = {'kernels': 'BOO gather pass (scattered matrix)' if gather else 'stripe',
+               'ms_per_step': round(p_wall, 5), 'kernel_ms_mean': round(p_ev, 5),
                'gflops': round(flops / (p_wall * 1e-3) / 1e9, 2),
                'hbm_gbs': round(balg / (p_ev * 1e-3) / 1e9, 1),
                'hbm_frac': round(balg / (p_ev * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),

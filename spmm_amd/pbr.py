@@ -33,6 +33,14 @@ __all__ = [
 ]
 
 LONG_ROW_THRESHOLD = 256   # longer remainder rows go to the split-row pass
+# A PBR matrix whose blocks hold less than this share of its entries (a
+# scattered matrix: most entries in the CSR remainder) is multiplied through
+# the BOO kernels instead: its whole CSR is staged at .to('cuda') as a BOO
+# staging without blocks (32-row slices), whose scattered rows the gather
+# pass walks in a Cuthill-McKee order when that keeps their X rows close
+# (permuted 27-point 128^3, K=32: the stripe kernel's remainder rounds take
+# 1.08 ms in row order).  Block-dominated matrices keep the stripe kernel.
+GATHER_MAX_BLOCK_SHARE = 0.25
 
 
 class DataOrder(enum.IntEnum):
@@ -170,8 +178,41 @@ def _pbr_to(self, device='cuda'):
     meta.stripe_ptr, meta.long_rows, meta.desc = _kernel_staging(
         int(self.rows), int(self.cols), int(self.block_rows), int(self.block_cols),
         d['block_coords'], d['remainder_indptr'], meta, device)
+    meta.gather = _gather_staging(self, device) if _scattered(self) else None
     self._gpu_meta = meta
     return self
+
+
+def _scattered(pbr_mat) -> bool:
+    """Most entries in the remainder (see GATHER_MAX_BLOCK_SHARE), and a CSR
+    the BOO staging takes (int32 positions and columns)."""
+    total = int(pbr_mat.total_nnz)
+    return (total > 0 and int(pbr_mat.compressed_nnz()) < GATHER_MAX_BLOCK_SHARE * total
+            and total < 2 ** 31 and int(pbr_mat.cols) < 2 ** 31 and int(pbr_mat.rows) < 2 ** 31)
+
+
+def _gather_staging(pbr_mat, device):
+    """The whole matrix as a BOO staging without blocks: every entry in the
+    remainder CSR (pbr_to_csr's), identity 32-row slices.  Returns the staged
+    tensors and the BOO launch descriptor (``desc``)."""
+    from . import boo as _boo
+    csr = pbr_to_csr(pbr_mat)
+    rows, cols = int(pbr_mat.rows), int(pbr_mat.cols)
+    i32 = np.int32
+    val_t = np.dtype(pbr_mat.scalar_dtype)
+    grp = lambda n: np.r_[np.arange(0, n, 32), n].astype(i32)  # noqa: E731
+    d = {
+        'row_grp_ptr': grp(rows), 'row_ids': np.arange(rows, dtype=i32),
+        'col_grp_ptr': grp(cols), 'col_ids': np.arange(cols, dtype=i32),
+        'blk_row_grp': np.zeros(0, i32), 'blk_col_grp': np.zeros(0, i32), 'blk_nz_ptr': np.zeros(1, i32),
+        'blk_shift': np.zeros(0, np.uint8), 'nz_idx': np.zeros(0, np.uint16), 'nz_val': np.zeros(0, val_t),
+        'rem_indptr': csr.indptr.astype(i32), 'rem_col_ind': csr.indices.astype(i32),
+        'rem_vals': np.ascontiguousarray(csr.data, dtype=val_t),
+        'tail_row': np.zeros(0, i32), 'tail_col': np.zeros(0, i32), 'tail_val': np.zeros(0, val_t),
+    }
+    row_ids_dev = torch.arange(rows, dtype=torch.int32, device=device)
+    staged, rem_dev, desc = _boo._kernel_staging(rows, cols, d, True, row_ids_dev, device)
+    return types.SimpleNamespace(staged=staged, rem=rem_dev, row_ids=row_ids_dev, desc=desc)
 
 
 # ---------------------------------------------------------------------------
@@ -262,8 +303,16 @@ def pbr_batched_matmul_cuda(pbr_mat, x: torch.Tensor, csr_mode: int = 0,
         y = torch.empty((batch, pbr_mat.rows, K), dtype=x.dtype, device=x.device)
         if y.numel():
             stream = torch.cuda.current_stream(x.device).cuda_stream
-            core.pbr_matmul_gpu(meta.desc, _DTYPE_CODE[x.dtype], int(xc.data_ptr()),
-                                int(y.data_ptr()), batch, K, int(stream))
+            dt = _DTYPE_CODE[x.dtype]
+            if meta.gather is not None:   # a scattered matrix: the BOO gather pass (GATHER_MAX_BLOCK_SHARE)
+                gd = meta.gather.desc
+                ws_bytes = int(core.boo_workspace_bytes(gd, dt, batch, K))
+                ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
+                core.boo_matmul_gpu(gd, dt, int(xc.data_ptr()), int(y.data_ptr()), batch, K,
+                                    int(ws.data_ptr()) if ws is not None else 0, ws_bytes, int(stream))
+            else:
+                core.pbr_matmul_gpu(meta.desc, dt, int(xc.data_ptr()), int(y.data_ptr()), batch, K,
+                                    int(stream))
     return y
 
 
@@ -291,6 +340,9 @@ def pbr_launch_info(pbr_mat, features: int, batch: int = 1, x=None) -> list:
         raise RuntimeError("PBRMatrix is not on GPU. Call .to('cuda') first.")
     with torch.cuda.device(meta.codes.device):
         xp = int(x.data_ptr()) if x is not None else 0
+        if meta.gather is not None:
+            return core.boo_launch_info(meta.gather.desc, _DTYPE_CODE[meta.data.dtype], xp, 0, int(batch),
+                                        int(features))
         return core.pbr_launch_info(meta.desc, _DTYPE_CODE[meta.data.dtype], xp, 0, int(batch), int(features))
 
 

@@ -14,6 +14,18 @@ from oracle import oracle as O
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(autouse=True, params=['auto', 'stripe'])
+def pbr_route(request, monkeypatch):
+    """Run every PBR case twice: with the default route (a matrix whose
+    blocks hold few of its entries runs its CSR through the BOO gather pass)
+    and with the stripe kernel forced for every matrix."""
+    if request.param == 'stripe':
+        if 'pbr' not in request.node.name:
+            pytest.skip('the route applies to PBR only')
+        monkeypatch.setattr(SP, 'GATHER_MAX_BLOCK_SHARE', 0.0)
+    return request.param
+
+
 def check(y, A, x):
     tol = 1e-5 if y.dtype == torch.float32 else 1e-12
     ratio, ok = O.within_bound(y.detach().cpu().numpy(), A, x.detach().cpu().numpy(), tol)
@@ -152,3 +164,28 @@ def test_csr_naive(index_dtype, data_dtype, kind, n, features):
     y = S.spdmm_csr_naive(t, x)
     check(y, A, x)
     torch.testing.assert_close(y.cpu(), torch.sparse.mm(t.cpu(), x.cpu()))
+
+
+@pytest.mark.parametrize('dtype', [np.float32, np.float64])
+def test_pbr_scattered_matrix_route(pbr_route, dtype):
+    """A permuted 27-point stencil keeps 5 % of its entries in 8x8 blocks: by
+    default its whole CSR runs through the BOO gather pass (launch_info names
+    those kernels); an unpermuted one, 96 % in blocks, keeps the stripe
+    kernel.  Both within the bound, batch 2."""
+    from spmm_amd import matrices as M
+    K = 32
+    for A, scattered in ((M.permuted(M.stencil_27pt(16, dtype=dtype), seed=1), True),
+                         (M.stencil_27pt(16, dtype=dtype), False)):
+        p = S.csr_to_pbr(A, 8, 8, 4).to('cuda')
+        gather = scattered and pbr_route == 'auto'
+        assert (p._gpu_meta.gather is not None) == gather
+        tdt = torch.float32 if dtype == np.float32 else torch.float64
+        x = torch.randn((2, A.shape[1], K), dtype=tdt, device='cuda')
+        y = S.pbr_matmul(p, x)
+        for b in range(2):
+            check(y[b], A, x[b])
+        names = [k['kernel'] for k in S.pbr_launch_info(p, K, batch=2, x=x)]
+        assert ('pbr_stripe_kernel' in names) == (not gather)
+        if gather:
+            assert 'boo_rows_kernel' in names
+        assert torch.equal(S.pbr_matmul(p, x), y)
