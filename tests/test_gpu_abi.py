@@ -147,14 +147,18 @@ def _boo_call(lib, desc, X, Y, K, ws=None, wsb=0):
                                P_(stream))
 
 
-@pytest.mark.parametrize('case', ['stencil', 'permuted_half', 'permuted'])
+@pytest.mark.parametrize('case', ['stencil', 'permuted_half', 'permuted', 'rmat'])
 def test_boo_through_raw_c_abi(lib, case):
     """cases: a stencil (tile stream only), a stencil whose second half is
-    permuted (tile stream and gather rows), a permuted stencil (gather rows)."""
+    permuted (tile stream and gather rows), a permuted stencil (gather rows),
+    an R-MAT graph (gather rows, chunk tasks with the hot-column launch order
+    copied out by spmm_boo_stage_copy_gtask_order)."""
     dev = torch.device('cuda', 0)
     A0 = M.stencil_27pt(16)
     if case == 'stencil':
         A = A0
+    elif case == 'rmat':
+        A = M.rmat(scale=17, edge_factor=8, seed=3)
     elif case == 'permuted':
         A = M.permuted(A0, seed=2)
     else:
@@ -167,6 +171,8 @@ def test_boo_through_raw_c_abi(lib, case):
     desc, info = stage_boo_via_c(lib, boo, dev, keep)
     if case == 'stencil':
         assert info.n_crow == 0 and info.n_stream_rows == A.shape[0]
+    elif case == 'rmat':
+        assert info.n_gtask_order == info.n_gtask > 0 and desc.gtask_order
     elif case == 'permuted':
         assert info.n_crow == A.shape[0]
     else:

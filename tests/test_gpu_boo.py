@@ -455,20 +455,21 @@ def test_hot_column_tasks_first(path):
     from spmm_amd import matrices as M
     from spmm_amd._native import core
     A = M.rmat(scale=17, edge_factor=8, seed=3)
-    K = 64
-    x = torch.from_numpy(np.random.default_rng(1).standard_normal((A.shape[1], K)).astype(np.float32)).cuda()
+    K, B = 64, 2
+    x = torch.from_numpy(np.random.default_rng(1).standard_normal((B, A.shape[1], K)).astype(np.float32)).cuda()
     boo = S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32).to('cuda')
     y = S.boo_matmul(boo, x)
-    check(y, A, x)
+    for b in range(B):
+        check(y[b], A, x[b])
     desc = boo._gpu_meta.desc
     if path == 'gather':
         assert desc['gtask_order'] != 0
     if desc['gtask_order']:
         plain = dict(desc, gtask_order=0)
         y2 = torch.empty_like(y)
-        wsb = int(core.boo_workspace_bytes(plain, 0, 1, K))
+        wsb = int(core.boo_workspace_bytes(plain, 0, B, K))
         ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device='cuda')
-        core.boo_matmul_gpu(plain, 0, int(x.data_ptr()), int(y2.data_ptr()), 1, K, int(ws.data_ptr()), wsb,
+        core.boo_matmul_gpu(plain, 0, int(x.data_ptr()), int(y2.data_ptr()), B, K, int(ws.data_ptr()), wsb,
                             int(torch.cuda.current_stream().cuda_stream))
         torch.cuda.synchronize()
         assert torch.equal(y, y2)
