@@ -1411,20 +1411,31 @@ __global__ void __launch_bounds__(256) gather_chunk_kernel(const int* __restrict
 }
 
 // Long gather row i: Y[crow_id[r0 + i]] = sum of its tasks' partial rows, in
-// task order (deterministic).
-template <typename T>
+// task order (deterministic).  LPR lanes per row, VEC features per lane,
+// 256 / LPR rows per workgroup; rows wider than LPR * VEC features loop.
+template <typename T, int VEC, int LPR>
 __global__ void __launch_bounds__(256) gather_fix_kernel(const int* __restrict__ gtask_ptr,
-                                                         const int* __restrict__ crow_id, int r0,
+                                                         const int* __restrict__ crow_id, int r0, int n_long,
                                                          const T* __restrict__ P, T* __restrict__ Y,
                                                          int rows, int K, int batch) {
-    const int i = blockIdx.x;
+    constexpr int RPB = 256 / LPR;
+    const int i = (int)blockIdx.x * RPB + (int)threadIdx.x / LPR;
+    if (i >= n_long) return;  // no barriers below
+    const int l = threadIdx.x % LPR;
     const int b = blockIdx.z;
     const int yrow = crow_id[r0 + i];
     const int t0 = gtask_ptr[i], t1 = gtask_ptr[i + 1];
-    for (int f = threadIdx.x; f < K; f += blockDim.x) {
-        T sum = T(0);
-        for (int t = t0; t < t1; ++t) sum += P[((size_t)t * batch + b) * K + f];
-        Y[((size_t)b * rows + yrow) * K + f] = sum;
+    for (int f = l * VEC; f < K; f += LPR * VEC) {  // K is a multiple of VEC
+        T sum[VEC];
+#pragma unroll
+        for (int u = 0; u < VEC; ++u) sum[u] = T(0);
+        for (int t = t0; t < t1; ++t) {
+            T p[VEC];
+            load_vec<T, VEC>(P + ((size_t)t * batch + b) * K + f, p);
+#pragma unroll
+            for (int u = 0; u < VEC; ++u) sum[u] += p[u];
+        }
+        store_vec<T, VEC>(Y + ((size_t)b * rows + yrow) * K + f, sum);
     }
 }
 
@@ -1927,6 +1938,26 @@ int launch_boo_rows_v(const spmm_boo_desc* A, const T* X, T* Y, int K, int batch
     return launch_boo_rows_l<T, VEC, 64>(A, X, Y, K, batch, s);
 }
 
+template <typename T, int VEC, int LPR>
+int launch_gather_fix_l(const spmm_boo_desc* A, const T* P2, T* Y, int K, int batch, hipStream_t s) {
+    constexpr int RPB = 256 / LPR;
+    const int n_long = A->n_crow_long;
+    const dim3 grid(round_up8((n_long + RPB - 1) / RPB), 1, batch);
+    return launch("gather_fix_kernel", gather_fix_kernel<T, VEC, LPR>, grid, dim3(256), s, A->gtask_ptr,
+                  A->crow_id, A->n_crow - n_long, n_long, P2, Y, A->rows, K, batch);
+}
+
+// The fixup of the chunk tasks: lanes for the whole row (at most 64).
+template <typename T, int VEC>
+int launch_gather_fix_v(const spmm_boo_desc* A, const T* P2, T* Y, int K, int batch, hipStream_t s) {
+    const int need = (K + VEC - 1) / VEC;
+    if (need <= 4) return launch_gather_fix_l<T, VEC, 4>(A, P2, Y, K, batch, s);
+    if (need <= 8) return launch_gather_fix_l<T, VEC, 8>(A, P2, Y, K, batch, s);
+    if (need <= 16) return launch_gather_fix_l<T, VEC, 16>(A, P2, Y, K, batch, s);
+    if (need <= 32) return launch_gather_fix_l<T, VEC, 32>(A, P2, Y, K, batch, s);
+    return launch_gather_fix_l<T, VEC, 64>(A, P2, Y, K, batch, s);
+}
+
 template <typename T>
 int launch_boo_rows(const spmm_boo_desc* A, const T* X, T* Y, int K, int batch, T* P2, hipStream_t s) {
     constexpr int V = 16 / sizeof(T);
@@ -1942,8 +1973,8 @@ int launch_boo_rows(const spmm_boo_desc* A, const T* X, T* Y, int K, int batch, 
                           A->gtask_order, A->ccol, static_cast<const T*>(A->cval), X, P2, A->cols, K, batch);
         if (rc) return rc;
     }
-    return launch("gather_fix_kernel", gather_fix_kernel<T>, dim3(A->n_crow_long, 1, batch), dim3(256), s,
-                  A->gtask_ptr, A->crow_id, A->n_crow - A->n_crow_long, (const T*)P2, Y, A->rows, K, batch);
+    return vec && aligned16(P2) ? launch_gather_fix_v<T, V>(A, P2, Y, K, batch, s)
+                                : launch_gather_fix_v<T, 1>(A, P2, Y, K, batch, s);
 }
 
 template <typename T>
