@@ -1388,12 +1388,24 @@ __global__ void __launch_bounds__(256) gather_chunk_kernel(const int* __restrict
 #pragma unroll
                 for (int e = 0; e < VEC; ++e) acc[e] += v[u] * x[u][e];
         }
-        for (; j < e1; j += SLOTS) {
-            T x[VEC];
-            load_vec<T, VEC>(Xb + (size_t)ccol[j] * K + f, x);
-            const T v = cval[j];
+        if (j < e1) {
+            // the last (partial) round: every slot's remaining entries in
+            // flight at once; entries past the task's end repeat its first
+            // column (an L1 hit) with value 0
+            int c[U - 1];
+            T v[U - 1], x[U - 1][VEC];
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) acc[e] += v * x[e];
+            for (int u = 0; u < U - 1; ++u) {
+                const int jj = j + u * SLOTS;
+                c[u] = ccol[jj < e1 ? jj : e0];
+                v[u] = jj < e1 ? cval[jj] : T(0);
+            }
+#pragma unroll
+            for (int u = 0; u < U - 1; ++u) load_vec<T, VEC>(Xb + (size_t)c[u] * K + f, x[u]);
+#pragma unroll
+            for (int u = 0; u < U - 1; ++u)
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) acc[e] += v[u] * x[u][e];
         }
     }
 #pragma unroll
