@@ -74,8 +74,8 @@ constexpr int GATHER_SKEWED_LONG = 32;
 // Chunk tasks read X rows at random from every column, and on a power-law
 // graph a few columns carry much of the entries, yet in one pass their X rows
 // keep being evicted from L2 by the cold gathers in between (R-MAT 2^20: the
-// 16,384 most used columns carry 55 % of the entries, the chunk pass hits L2
-// on ~40 % of its reads).  When the GATHER_HOT_COLS most used columns of the
+// 16,384 most used columns carry 55 % of the entries, yet an LRU model of
+// the chunk pass hits L2 on only ~40 % of its reads).  When the GATHER_HOT_COLS most used columns of the
 // long gather rows carry at least GATHER_HOT_SHARE of their entries (and
 // GATHER_HOT_SKEW times their share of the columns), each long row's entries
 // in those columns come first, in their own chunk tasks, and every such task
@@ -608,7 +608,10 @@ private:
         // the GATHER_HOT_COLS most used columns (ties: lower column first)
         std::vector<int32_t> ids((size_t)cols);
         for (int32_t c = 0; c < cols; ++c) ids[(size_t)c] = c;
-        auto more_used = [&](int32_t a, int32_t b) { return cnt[(size_t)a] != cnt[(size_t)b] ? cnt[(size_t)a] > cnt[(size_t)b] : a < b; };
+        auto more_used = [&](int32_t a, int32_t b) {
+            const int32_t ca = cnt[(size_t)a], cb = cnt[(size_t)b];
+            return ca != cb ? ca > cb : a < b;
+        };
         std::nth_element(ids.begin(), ids.begin() + (GATHER_HOT_COLS - 1), ids.end(), more_used);
         std::vector<uint8_t> hot((size_t)cols, 0);
         long long n_in = 0;
