@@ -15,10 +15,13 @@ time: ``spmm_amd`` loads what is here and fails loudly when it is missing.
 Host-code sanitizers (CPU only; the GPU code is never built with them):
 
 * ``python spmm_amd/build.py core-san`` -- ``_core`` with AddressSanitizer and
-  UBSan (every UB check fatal) into ``_build/san/``;
+  UBSan (every UB check fatal) into ``_build/san/``, linked against a copy of
+  the C ABI library whose host code (the tile-stream staging among it) is
+  built with the same checks (``libspmm_amd_san.so``);
 * ``python spmm_amd/build.py san-test [pytest args]`` -- builds it and runs
   ``pytest -m "not gpu"`` with that module loaded in place of ``_core``
-  (``SPMM_AMD_CORE``) and the sanitizer runtimes preloaded into Python.
+  (``SPMM_AMD_CORE``), the tests that open the C ABI with ctypes on that
+  library (``SPMM_AMD_LIB``), and the sanitizer runtimes preloaded into Python.
 """
 
 from __future__ import annotations
@@ -64,28 +67,42 @@ def _hipcc():
     return 'hipcc'
 
 
-def build_hip():
+def build_hip(out=HIP_LIB, extra=()):
     srcs = [CSRC / 'spmm_kernels.hip', CSRC / 'measure.hip']
     # measure.hip opens librocsparse with dlopen: link libdl only
-    _run([_hipcc(), *HIPCC_FLAGS, f'-I{INCLUDE}', *srcs, '-o', HIP_LIB, '-ldl'])
+    _run([_hipcc(), *HIPCC_FLAGS, *extra, f'-I{INCLUDE}', *srcs, '-o', out, '-ldl'])
 
 
-def build_core(out=CORE_LIB, flags=CXX_FLAGS, rpath='$ORIGIN'):
+def build_core(out=CORE_LIB, flags=CXX_FLAGS, rpath='$ORIGIN', lib='spmm_amd', libdir=HERE):
     import pybind11
     src = CSRC / 'core.cpp'
     py_inc = sysconfig.get_paths()['include']
     _run(['g++', *flags, f'-I{INCLUDE}', f'-I{CSRC}', f'-I{pybind11.get_include()}',
-          f'-I{py_inc}', src, '-o', out, f'-L{HERE}', '-lspmm_amd', f'-Wl,-rpath,{rpath}'])
+          f'-I{py_inc}', src, '-o', out, f'-L{libdir}', f'-l{lib}', f'-Wl,-rpath,{rpath}'])
 
 
-SAN_CORE = ROOT / '_build' / 'san' / CORE_LIB.name
+SAN_DIR = ROOT / '_build' / 'san'
+SAN_CORE = SAN_DIR / CORE_LIB.name
 SAN_FLAGS = ['-O1', '-g', '-fno-omit-frame-pointer', '-fsanitize=address,undefined',
              '-fno-sanitize-recover=all', *[f for f in CXX_FLAGS if f != '-O3']]
+# The C ABI library again with its host code -- the tile-stream staging, the
+# entry points' checks -- under the same sanitizers; each flag is passed to
+# the host compilation only (-Xarch_host), the GPU code is built as usual.
+SAN_LIB = SAN_DIR / 'libspmm_amd_san.so'
+# The runtimes preloaded are gcc's (the core is built by g++); clang's
+# function-type check is the one UBSan check they have no handler for.
+SAN_HOST_FLAGS = ['-Xarch_host', '-g', '-Xarch_host', '-fno-omit-frame-pointer',
+                  '-Xarch_host', '-fsanitize=address',
+                  '-Xarch_host', '-fsanitize=undefined',
+                  '-Xarch_host', '-fno-sanitize=function',
+                  '-Xarch_host', '-fno-sanitize-recover=all',
+                  f'-Wl,-soname,{SAN_LIB.name}']
 
 
 def build_core_san():
-    SAN_CORE.parent.mkdir(parents=True, exist_ok=True)
-    build_core(SAN_CORE, SAN_FLAGS, str(HERE))
+    SAN_DIR.mkdir(parents=True, exist_ok=True)
+    build_hip(SAN_LIB, SAN_HOST_FLAGS)
+    build_core(SAN_CORE, SAN_FLAGS, str(SAN_DIR), lib='spmm_amd_san', libdir=SAN_DIR)
 
 
 def san_env():
@@ -95,7 +112,7 @@ def san_env():
                               text=True).stdout.strip()
         runtimes.append(path)
     env = dict(os.environ)
-    env.update(SPMM_AMD_CORE=str(SAN_CORE), LD_PRELOAD=' '.join(runtimes),
+    env.update(SPMM_AMD_CORE=str(SAN_CORE), SPMM_AMD_LIB=str(SAN_LIB), LD_PRELOAD=' '.join(runtimes),
                # Python and torch are not instrumented: their allocations are
                # outside the checks, and their exit-time leaks are not ours
                ASAN_OPTIONS='detect_leaks=0:alloc_dealloc_mismatch=0:abort_on_error=1',

@@ -576,10 +576,18 @@ __device__ __forceinline__ void group_sync() {
 // item's tiles and stores them once, at the item's last tile (to Y, or to a
 // partial slot of a split item).  Steps past the end of the stream load its
 // last tile (the data is never used) and store nothing.
-// fp64 with 16 features per lane: 2 waves per SIMD, room for the 64
-// accumulators and the X staging registers without spilling.
+// Waves per SIMD the kernel is compiled for, as many as its registers allow
+// without spilling: fp64 with 16 features per lane 2 (the 64 accumulators and
+// the X staging registers), with 8 features 3; a one-wave workgroup of float
+// 64-feature tiles stages all 32 X columns itself, 2.
+template <typename T, int F, int VEC, int WG>
+constexpr int stream_occupancy() {
+    if (sizeof(T) == 8) return F >= 16 ? 2 : F >= 8 ? 3 : 4;
+    return F >= 32 && WG == 1 ? 2 : 4;
+}
+
 template <typename T, int F, int VEC, int D, int DF, int WG, bool FULL, bool A32>
-__global__ void __launch_bounds__(64 * WG, sizeof(T) == 8 && F >= 16 ? 2 : 4) boo_stream_kernel(StreamArgs<T> a,
+__global__ void __launch_bounds__(64 * WG, (stream_occupancy<T, F, VEC, WG>())) boo_stream_kernel(StreamArgs<T> a,
                                                                                                   int kt0) {
     typedef BooGeom<T, F, VEC> G;
     constexpr int NW = G::NST / WG;   // X staging instructions per wave

@@ -2,6 +2,7 @@
 declares; its host-only entry points work without a GPU."""
 
 import ctypes
+import os
 import re
 from pathlib import Path
 
@@ -10,7 +11,9 @@ import pytest
 
 ROOT = Path(__file__).resolve().parents[1]
 HEADER = ROOT / 'include' / 'spmm_amd.h'
-LIB = ROOT / 'spmm_amd' / 'libspmm_amd.so'
+# SPMM_AMD_LIB: another build of the library (the host-sanitized one of
+# `python spmm_amd/build.py san-test`)
+LIB = Path(os.environ['SPMM_AMD_LIB']) if os.environ.get('SPMM_AMD_LIB') else ROOT / 'spmm_amd' / 'libspmm_amd.so'
 
 
 def declared_functions():

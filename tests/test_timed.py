@@ -6,6 +6,7 @@ harnesses validate in the reference's order with its messages
 test_gpu_timed.py."""
 
 import ctypes
+import os
 from pathlib import Path
 
 import numpy as np
@@ -15,7 +16,10 @@ import torch
 
 import spmm_amd as S
 
-LIB = Path(__file__).resolve().parents[1] / 'spmm_amd' / 'libspmm_amd.so'
+# SPMM_AMD_LIB: another build of the library (the host-sanitized one of
+# `python spmm_amd/build.py san-test`)
+LIB = (Path(os.environ['SPMM_AMD_LIB']) if os.environ.get('SPMM_AMD_LIB')
+       else Path(__file__).resolve().parents[1] / 'spmm_amd' / 'libspmm_amd.so')
 
 
 @pytest.fixture(scope='module')
