@@ -4,8 +4,9 @@ same X, bit-equal Y (the same kernels run; only the workspace's memory
 differs), on two calls in a row, the second with a smaller input.  The
 stagings are chosen so that the workspace is really used: slices heavier
 than the item limit (partial slots added by the fixup pass) and long gather
-rows (chunk tasks' partial rows).  A call whose workspace would exceed the
-scratch is refused before any work is enqueued."""
+rows (chunk tasks' partial rows, also in the hot-column launch order).  A
+call whose workspace would exceed the scratch is refused before any work is
+enqueued."""
 
 import ctypes as C
 from pathlib import Path
@@ -38,8 +39,10 @@ def _matrix(kind):
     if kind == 'heavy_slices':          # 32-row slices of ~6,500 entries: split into items
         A = sp.random(4096, 2048, density=0.1, format='csr', random_state=np.random.default_rng(7),
                       dtype=np.float32)
-    else:                               # power-law rows: long gather rows cut into chunk tasks
+    elif kind == 'long_gather_rows':    # power-law rows: long gather rows cut into chunk tasks
         A = M.rmat(13, 16, seed=3)
+    else:                               # 2^17 columns: hot-column chunk tasks launched first
+        A = M.rmat(17, 8, seed=3)
     return sp.csr_matrix(A, dtype=np.float32)
 
 
@@ -65,7 +68,7 @@ def _run(lib, desc, X, K, batch, noalloc):
     return Y
 
 
-@pytest.mark.parametrize('kind', ['heavy_slices', 'long_gather_rows'])
+@pytest.mark.parametrize('kind', ['heavy_slices', 'long_gather_rows', 'hot_column_tasks'])
 def test_noalloc_matches_workspace_entry_point(lib, kind):
     dev = torch.device('cuda', 0)
     A = _matrix(kind)
@@ -75,6 +78,8 @@ def test_noalloc_matches_workspace_entry_point(lib, kind):
         assert desc.n_slots > 0
     else:
         assert desc.n_gtask > 0
+    if kind == 'hot_column_tasks':
+        assert desc.gtask_order
     # two calls in a row, the second smaller (batch and K)
     for batch, K in ((2, 96), (1, 24)):
         wsb = lib.spmm_boo_workspace_bytes(C.byref(desc), 0, C.c_int64(batch), C.c_int64(K))
