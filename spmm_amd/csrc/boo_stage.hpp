@@ -59,6 +59,16 @@ constexpr int SERIAL_MAX_BUSY = 4;    // busy rows a serial tile may have
 // a step (X tile staged, workgroup synchronised) and finishing an item.
 constexpr long long COST_STEP = 256;
 constexpr long long COST_ITEM = 512;
+// A group's members all end their item at its last step, so in a uniform
+// matrix every wave stores its 32 Y rows in the same step and the stores
+// leave in one burst that the next step's loads queue behind.  In a group of
+// at least EARLY_STORE_MIN_STEPS steps, its shared remainder tiles are walked
+// first and each member stores at its own last tile with entries: in a
+// stencil the members of the lower plane then finish a few steps before the
+// others and the burst splits (27-point 64^3, K=64: -1 to -2.3 us).  Short
+// groups keep one store step (5-point 256^2, K=128: 16.4 -> 18.0 us
+// otherwise).
+constexpr size_t EARLY_STORE_MIN_STEPS = 12;
 
 // Gather-pass rows longer than the long-row threshold are summed in chunks of
 // at most GATHER_CHUNK entries, one workgroup each, into partial rows that a
@@ -267,6 +277,7 @@ private:
         size_t s0, s1;  // steps in steps_
         long long cost;
         int slot;       // -1: stores Y; else the partial slot of an item of a split slice
+        bool early = false;  // members store at their own last tile with entries
     };
 
     // Every index the staging later uses to address a host array is checked
@@ -877,6 +888,7 @@ private:
             add_steps(c0.cid_off, c0.nc, range);
             i = j;
         }
+        const size_t b_end = steps_.size();
         // short remainder rows: tiles over the members' distinct columns
         std::vector<int32_t> ucols;
         for (int m = 0; m < g.n_members; ++m) {
@@ -911,6 +923,9 @@ private:
             for (auto& r : range) r = {0, 0};
             add_steps(0, 0, range);
         }
+        g.early = steps_.size() - g.s0 >= EARLY_STORE_MIN_STEPS;
+        if (g.early && b_end > g.s0)  // the remainder tiles first
+            std::rotate(steps_.begin() + (std::ptrdiff_t)g.s0, steps_.begin() + (std::ptrdiff_t)b_end, steps_.end());
         g.s1 = steps_.size();
         // A step costs about the same whatever its entries (the X tile is
         // loaded and the workgroup synchronises either way), and entries add
@@ -1079,10 +1094,21 @@ private:
                     const bool real = m < g.n_members;
                     const Slice* sl = real ? &slices_[g.members[m]] : nullptr;
                     const int row_off = real ? sl->row_off : 0, nr = real ? sl->nr : 0;
+                    // the step at which this member stores (see EARLY_STORE_MIN_STEPS)
+                    size_t store_at = g.s1 - 1;
+                    if (g.early && real) {
+                        for (size_t st = g.s1; st-- > g.s0;) {
+                            const Piece& pc = pieces_[steps_[st].m0 + m];
+                            if (pc.e1 > pc.e0) {
+                                store_at = st;
+                                break;
+                            }
+                        }
+                    }
                     for (size_t st = g.s0; st < g.s1; ++st) {
                         const Step& sp = steps_[st];
                         const Piece& pc = pieces_[sp.m0 + m];
-                        const uint32_t flags = st + 1 == g.s1 ? FLAG_LAST : 0u;
+                        const uint32_t flags = st == store_at ? FLAG_LAST : 0u;
                         emit_tile(S, real ? pc : Piece{0, 0}, sp.cid_off, sp.nc, row_off, nr, flags, real ? g.slot : -1);
                     }
                 }

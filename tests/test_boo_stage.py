@@ -94,11 +94,24 @@ def check_stream(A, boo, max_item_nnz=4096, long_thr=256, n_waves=64, group=1, m
     if len(tiles) == 0:
         assert st['n_waves'] == 0 and list(wt) == [0]
         return st
-    assert last[-1] == 1
     assert wt[0] == 0 and wt[-1] == len(tiles) and np.all(np.diff(wt) > 0)
     assert st['n_waves'] == len(wt) - 1 <= max(n_waves, group) and st['n_waves'] % group == 0
-    for w in range(1, len(wt) - 1):
-        assert last[wt[w] - 1] == 1                    # waves hold whole items
+    # waves hold whole items: a wave's stream splits at its storing tiles into
+    # runs whose tiles with entries all belong to one slice, and after its
+    # last storing tile come only tiles without entries (a member of a long
+    # group stores at its own last tile with entries)
+    nnz_t = tiles[:, 1] & 0xff
+    for w in range(len(wt) - 1):
+        idx = np.arange(wt[w], wt[w + 1])
+        stores = idx[last[idx] == 1]
+        assert len(stores) > 0
+        assert np.all(nnz_t[stores[-1] + 1:wt[w + 1]] == 0)
+        a = wt[w]
+        for e in stores:
+            run = np.arange(a, e + 1)
+            busy = run[nnz_t[run] > 0]
+            assert len(set(tiles[busy, 3].tolist())) <= 1
+            a = e + 1
     # the waves of a workgroup walk equal-length streams over the same X tiles
     lens = np.diff(wt).reshape(-1, group)
     assert np.all(lens == lens[:, :1])
