@@ -378,6 +378,71 @@ def test_gather_pass_hot_columns_first():
     assert st['n_crow_long'] > 1000 and len(st['gtask_order']) == 0
 
 
+def _hot_edge_matrix(seed=0):
+    """40,000 x 262,144.  Long rows: 400 over 100 hot columns each (windows
+    that cover columns 0-16,383 at least twice), 400 over 50 cold ones, 400
+    over 40 hot and 30 cold, and row 3 over 1,500 hot and 900 cold (longer
+    than a chunk task on both sides); cold columns (from 131,072 up) are each
+    used once, so the 16,384 most used columns are exactly 0-16,383.  The
+    other rows hold 3 hot entries."""
+    rng = np.random.default_rng(seed)
+    n, cols, H = 40000, 1 << 18, 16384
+    cold = iter(range(1 << 17, 1 << 18))
+    win = iter(range(0, 10 ** 9, 100))
+    rows, cc = [], []
+    for r in range(n):
+        if r == 3:
+            c = np.concatenate([rng.choice(H, 1500, replace=False), [next(cold) for _ in range(900)]])
+        elif r % 100 == 0:
+            w = next(win)
+            c = (w + np.arange(100)) % H
+        elif r % 100 == 1:
+            c = np.array([next(cold) for _ in range(50)])
+        elif r % 100 == 2:
+            c = np.concatenate([rng.choice(H, 40, replace=False), [next(cold) for _ in range(30)]])
+        else:
+            c = rng.choice(H, 3, replace=False)
+        rows.append(np.full(len(c), r))
+        cc.append(np.asarray(c))
+    r = np.concatenate(rows)
+    c = np.concatenate(cc)
+    v = rng.standard_normal(len(r)).astype(np.float32)
+    A = sp.csr_matrix((v, (r, c)), shape=(n, cols))
+    A.sum_duplicates()
+    A.sort_indices()
+    return A
+
+
+def test_gather_pass_hot_split_edge_rows():
+    # long rows all in hot columns, all in cold ones, both, and one longer than
+    # a chunk task: every task one kind, each row's hot tasks first, the rows'
+    # entries unchanged (check_stream), all hot tasks launched first
+    A = _hot_edge_matrix()
+    boo = S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32)
+    st = check_stream(A, boo, long_thr=256, min_reuse=1.5, group=4)
+    gt = st['gtask'].reshape(-1, 2)
+    go = st['gtask_order']
+    n_long = st['n_crow_long']
+    assert n_long == 1201 and len(go) == len(gt)
+    cp = st['crow_ptr']
+    first = cp[len(cp) - 1 - n_long]
+    hot = _hot_columns(st['ccol'][first:], A.shape[1], 16384)
+    assert np.array_equal(np.nonzero(hot)[0], np.arange(16384))
+    kind = np.array([int(hot[st['ccol'][a:b]].all()) - int((~hot[st['ccol'][a:b]]).all()) for a, b in gt])
+    assert np.all(kind != 0)
+    n_hot = int((kind == 1).sum())
+    assert np.all(kind[go[:n_hot]] == 1) and np.all(kind[go[n_hot:]] == -1)
+    gp = st['gtask_ptr']
+    row_of = st['crow_id'][len(st['crow_id']) - n_long:]
+    kinds = {}
+    for i in range(n_long):
+        k = kind[gp[i]:gp[i + 1]]
+        assert np.all(np.diff(k) <= 0)
+        kinds[int(row_of[i]) % 100 if row_of[i] != 3 else 'big'] = (int((k == 1).sum()), int((k == -1).sum()))
+    assert kinds[0] == (1, 0) and kinds[1] == (0, 1) and kinds[2] == (1, 1)
+    assert kinds['big'][0] >= 2 and kinds['big'][1] >= 1        # cut into chunks on both sides
+
+
 def test_gather_rows_reordered_when_it_keeps_x_rows_close():
     # A randomly permuted path graph (tridiagonal, 200,000 rows): in row order
     # the rows naming any X row lie ~67,000 rows apart, beyond the staging's

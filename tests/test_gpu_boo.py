@@ -473,3 +473,29 @@ def test_hot_column_tasks_first(path):
                             int(torch.cuda.current_stream().cuda_stream))
         torch.cuda.synchronize()
         assert torch.equal(y, y2)
+
+
+def test_hot_split_edge_rows(path):
+    """Long rows all in hot columns, all in cold ones, both, and one longer
+    than a chunk task on both sides (tests/test_boo_stage.py's matrix): within
+    the bound, and bit-equal to the same staging run in task order."""
+    from test_boo_stage import _hot_edge_matrix
+    from spmm_amd._native import core
+    A = _hot_edge_matrix()
+    K = 64
+    x = torch.from_numpy(np.random.default_rng(2).standard_normal((A.shape[1], K)).astype(np.float32)).cuda()
+    boo = S.csr_to_boo(A, cluster='identity', target_nr=32, target_nc=32).to('cuda')
+    y = S.boo_matmul(boo, x)
+    check(y, A, x)
+    desc = boo._gpu_meta.desc
+    if path == 'gather':
+        assert desc['gtask_order'] != 0
+    if desc['gtask_order']:
+        plain = dict(desc, gtask_order=0)
+        y2 = torch.empty_like(y)
+        wsb = int(core.boo_workspace_bytes(plain, 0, 1, K))
+        ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device='cuda')
+        core.boo_matmul_gpu(plain, 0, int(x.data_ptr()), int(y2.data_ptr()), 1, K, int(ws.data_ptr()), wsb,
+                            int(torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        assert torch.equal(y, y2)
