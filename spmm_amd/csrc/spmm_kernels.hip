@@ -1701,16 +1701,23 @@ __device__ __forceinline__ void pbr_stripe_body(const PbrArgs<T, I>& a, int stri
                 // (3) walk block blk
                 if (active) {
                     uint32_t rb = (uint32_t)((code >> (BR * r)) & rowbits);
+                    // an entry's first feature chunk at one multiply-add from
+                    // this lane's base in the tile, the others at fixed
+                    // per-lane distances from it
+                    const T* t0 = tile + fofs(0);
+                    int dq[G::NQ];
+#pragma unroll
+                    for (int q = 0; q < G::NQ; ++q) dq[q] = fofs(q) - fofs(0);
                     while (rb) {
                         const int c = __builtin_ctz(rb);
                         rb &= rb - 1u;
                         const T v = vb[r * BR + c];
-                        const T* xrow = tile + c * G::STRIDE;
+                        const T* x0 = t0 + c * G::STRIDE;
 #pragma unroll
                         for (int q = 0; q < G::NQ; ++q) {
                             if (FULL || fbase + fofs(q) < K) {
                                 T x[VEC];
-                                load_vec<T, VEC>(xrow + fofs(q), x);
+                                load_vec<T, VEC>(x0 + dq[q], x);
 #pragma unroll
                                 for (int u = 0; u < VEC; ++u) acc[q][u] += v * x[u];
                             }
