@@ -131,7 +131,7 @@ int spmm_boo_stage_sizes(const spmm_boo_stage* st, spmm_boo_stage_info* info);
 /* Host output arrays, sized from spmm_boo_stage_sizes:
  *   tiles [n_tiles*8] int32: ent_off, nnz | nc<<8 | nr<<16 | flags<<24, cid_off, row_off,
  *                            slot (-1: the item stores Y, else its partial slot), 0, 0, 0
- *   tile_rs [n_tiles*33] uint16, ent_val [n_ent] (dtype), ent_col [n_ent] uint8,
+ *   tile_rs [n_tiles*33] uint8, ent_val [n_ent] (dtype), ent_col [n_ent] uint8,
  *   tcols [n_tcols] int32, splits [n_splits*4] int32, long_rows [n_long] int32,
  *   wave_tiles [n_waves+1] int32,
  *   crow_ptr [n_crow+1] int32, crow_id [n_crow] int32, ccol [n_cnz] int32, cval [n_cnz] (dtype):
@@ -143,7 +143,7 @@ int spmm_boo_stage_sizes(const spmm_boo_stage* st, spmm_boo_stage_info* info);
  *   int32 (long row i owns tasks gtask_ptr[i] .. gtask_ptr[i+1]).
  * Every tile's entries start at an even index (odd tiles are followed by a
  * zero entry). */
-int spmm_boo_stage_copy(const spmm_boo_stage* st, int32_t* tiles, uint16_t* tile_rs,
+int spmm_boo_stage_copy(const spmm_boo_stage* st, int32_t* tiles, uint8_t* tile_rs,
                         void* ent_val, uint8_t* ent_col, int32_t* tcols, int32_t* splits,
                         int32_t* long_rows, int32_t* wave_tiles, int32_t* crow_ptr,
                         int32_t* crow_id, int32_t* ccol, void* cval, int32_t* gtask,
@@ -181,7 +181,7 @@ typedef struct spmm_boo_desc {
     const int32_t* row_ids;      /* [rows] */
     int32_t n_tiles;
     const int32_t* tiles;        /* [n_tiles*8] */
-    const uint16_t* tile_rs;     /* [n_tiles*33] */
+    const uint8_t* tile_rs;      /* [n_tiles*33] */
     const void* ent_val;         /* [n_ent] */
     const uint8_t* ent_col;      /* [n_ent] */
     const int32_t* tcols;        /* [n_tcols] */

@@ -49,6 +49,7 @@ namespace spmm_stage {
 constexpr int TILE_ROWS = 32;
 constexpr int TILE_COLS = 32;
 constexpr int TILE_ENT = 96;
+static_assert(TILE_ENT < 256, "tile row starts are stored in bytes");
 constexpr int TILE_RS = TILE_ROWS + 1;
 constexpr int TILE_WORDS = 8;
 constexpr uint32_t FLAG_LAST = 1u;    // last tile of its item
@@ -142,7 +143,7 @@ struct Staged {
     // [n_tiles][8]: ent_off, nnz|nc<<8|nr<<16|flags<<24, cid_off, row_off, slot, 0, 0, 0
     // (slot -1: the item stores Y; otherwise its partial slot)
     std::vector<int32_t> tiles;
-    std::vector<uint16_t> tile_rs;   // [n_tiles][33]: row starts relative to ent_off
+    std::vector<uint8_t> tile_rs;    // [n_tiles][33]: row starts relative to ent_off (<= TILE_ENT)
     std::vector<uint8_t> ent_col;    // [n_ent] (zero padding after odd tiles and at the end)
     std::vector<char> ent_val;       // [n_ent] values (float or double bytes)
     std::vector<int32_t> tcols;      // [cols + extra]: col_ids, then remainder tile columns
@@ -940,11 +941,11 @@ private:
                    int slot) {
         const int nnz = (int)(pc.e1 - pc.e0);
         const int ent_off = (int)S.ent_col.size();
-        uint16_t rs[TILE_RS];
+        uint8_t rs[TILE_RS];  // row starts fit a byte: TILE_ENT < 256
         int k = 0;
         for (int r = 0; r <= TILE_ROWS; ++r) {
             while (k < nnz && tent_[pc.e0 + k].lr < r) ++k;
-            rs[r] = (uint16_t)k;
+            rs[r] = (uint8_t)k;
         }
         for (size_t u = pc.e0; u < pc.e1; ++u) {
             const Ent& x = tent_[u];
@@ -1163,9 +1164,7 @@ private:
                 put32(rcontig ? (uint32_t)in_.row_ids[row_off] : (uint32_t)row_off);
                 if (nnz > 0)
                     for (int r = 0; r < TILE_ROWS; ++r) {
-                        const uint16_t v = S.tile_rs[(size_t)t * TILE_RS + r];
-                        if (v > 255) throw std::invalid_argument("tile row start exceeds a byte");
-                        rec.push_back((uint8_t)v);
+                        rec.push_back(S.tile_rs[(size_t)t * TILE_RS + r]);
                     }
                 for (int e = 0; e < nnz; ++e) rec.push_back(S.ent_col[(size_t)ent_off + e]);
                 while (rec.size() & 3) rec.push_back(0);

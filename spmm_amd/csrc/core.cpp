@@ -275,7 +275,7 @@ spmm_boo_desc boo_desc(const py::dict& d) {
     A.row_ids = reinterpret_cast<const int32_t*>(P(d, "row_ids"));
     A.n_tiles = d["n_tiles"].cast<int32_t>();
     A.tiles = reinterpret_cast<const int32_t*>(P(d, "tiles"));
-    A.tile_rs = reinterpret_cast<const uint16_t*>(P(d, "tile_rs"));
+    A.tile_rs = reinterpret_cast<const uint8_t*>(P(d, "tile_rs"));
     A.ent_val = reinterpret_cast<const void*>(P(d, "ent_val"));
     A.ent_col = reinterpret_cast<const uint8_t*>(P(d, "ent_col"));
     A.tcols = reinterpret_cast<const int32_t*>(P(d, "tcols"));
@@ -347,7 +347,7 @@ py::dict boo_stage(const py::dict& h, int32_t max_item_nnz, int32_t long_thresho
         splits((size_t)inf.n_splits * 4), longr((size_t)inf.n_long), wt((size_t)inf.n_waves + 1),
         crp((size_t)inf.n_crow + 1), cri((size_t)inf.n_crow), ccol((size_t)inf.n_cnz),
         gt((size_t)inf.n_gtask * 2), gtp((size_t)inf.n_crow_long + 1);
-    std::vector<uint16_t> rs((size_t)inf.n_tiles * 33);
+    std::vector<uint8_t> rs((size_t)inf.n_tiles * 33);
     std::vector<uint8_t> ecol((size_t)inf.n_ent);
     py::array ev = f64 ? py::array(py::array_t<double>((py::ssize_t)inf.n_ent))
                        : py::array(py::array_t<float>((py::ssize_t)inf.n_ent));

@@ -196,7 +196,7 @@ template <typename T>
 struct StreamArgs {
     int rows, cols, K, batch, n_waves, n_tiles, group;
     const int* tiles;           // 8 words: ent_off, nnz | nc<<8 | nr<<16 | flags<<24, cid_off, row_off, slot
-    const uint16_t* tile_rs;
+    const uint8_t* tile_rs;
     const T* ent_val;
     const uint8_t* ent_col;
     const int* tcols;
@@ -2311,7 +2311,7 @@ int spmm_boo_stage_sizes(const spmm_boo_stage* st, spmm_boo_stage_info* info) {
     return SPMM_OK;
 }
 
-int spmm_boo_stage_copy(const spmm_boo_stage* st, int32_t* tiles, uint16_t* tile_rs,
+int spmm_boo_stage_copy(const spmm_boo_stage* st, int32_t* tiles, uint8_t* tile_rs,
                         void* ent_val, uint8_t* ent_col, int32_t* tcols, int32_t* splits,
                         int32_t* long_rows, int32_t* wave_tiles, int32_t* crow_ptr, int32_t* crow_id,
                         int32_t* ccol, void* cval, int32_t* gtask, int32_t* gtask_ptr) {
@@ -2322,7 +2322,7 @@ int spmm_boo_stage_copy(const spmm_boo_stage* st, int32_t* tiles, uint16_t* tile
         return bytes == 0 || dst != nullptr;
     };
     bool ok = put(tiles, s.tiles.data(), s.tiles.size() * 4) &&
-              put(tile_rs, s.tile_rs.data(), s.tile_rs.size() * 2) &&
+              put(tile_rs, s.tile_rs.data(), s.tile_rs.size()) &&
               put(ent_val, s.ent_val.data(), s.ent_val.size()) &&
               put(ent_col, s.ent_col.data(), s.ent_col.size()) &&
               put(tcols, s.tcols.data(), s.tcols.size() * 4) &&

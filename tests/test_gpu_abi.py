@@ -100,7 +100,7 @@ def stage_boo_via_c(lib, boo, dev, keep):
     assert lib.spmm_boo_stage_sizes(st, C.byref(info)) == 0
     n = info
     out = {
-        'tiles': np.zeros(n.n_tiles * 8, i32), 'tile_rs': np.zeros(n.n_tiles * 33, np.uint16),
+        'tiles': np.zeros(n.n_tiles * 8, i32), 'tile_rs': np.zeros(n.n_tiles * 33, np.uint8),
         'ent_val': np.zeros(n.n_ent, np.float32), 'ent_col': np.zeros(n.n_ent, np.uint8),
         'tcols': np.zeros(n.n_tcols, i32), 'splits': np.zeros(n.n_splits * 4, i32),
         'long_rows': np.zeros(n.n_long, i32), 'wave_tiles': np.zeros(n.n_waves + 1, i32),
